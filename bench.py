@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Throughput of kern-glm53's `glm_deepgemm` fp8 GEMM path on one MI355X.
+
+One step = the fp8 GEMMs of one GLM-5.3 prefill chunk of M = 16384 rows at the reference's shapes
+(scripts/gen.py:181-195):
+  * dense  q_a/kv_a  (N=2624, ldc 2752, K=6144), q_b (N=16384, ldc 20480, K=2048), o_proj (N=6144, K=16384);
+  * MoE    gate_up   m-grouped psum GEMM over 256 experts, N=4096, K=6144, with the SiLU-mul + e4m3 requant
+           epilogue fused (writes the down-proj's operand), and down N=6144, K=2048, on the routing of 16384
+           tokens x top-8 drawn from a Zipf(1.1) expert popularity.
+value = algorithmic FLOPs of the step (2 M N K dense, 2 R N K over the R = 131072 routed rows for the MoE,
+padding excluded) / step time.  Operands are synthetic (seeded), generated and quantized on the GPU by the
+path's own quant / requant kernels, resident in HBM before timing.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+METRIC = "FP8 GEMM TFLOP/s + % MFMA peak: dense and 256-expert MoE at M=16384, 1 GPU"
+PEAK_FP8 = 5.0e15          # MI355X dense fp8 MFMA, FLOP/s
+PEAK_HBM = 8.0e12          # bytes/s
+M = 16384
+EXPERTS, TOPK, INTER, H = 256, 8, 2048, 6144
+DENSE = [  # name, n, k, ldc  (scripts/gen.py:183-186: a.shared, b.shared, o)
+    ("q_a_kv_a", 2624, 6144, 2752),
+    ("q_b", 16384, 2048, 20480),
+    ("o_proj", 6144, 16384, 6144),
+]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def prepare(dev):
+    from kern_glm53_amd import ops, synth
+
+    sfw = ops.sf_words
+    data = {}
+
+    def quant_act(K, seed):
+        x = synth.activations(M, K, synth.generator(seed, "cuda"), device=dev)
+        q = torch.empty(M, K, dtype=torch.uint8, device=dev)
+        sf = torch.empty(sfw(K) * M * 4, dtype=torch.uint8, device=dev)
+        ops.quant(x, K, q, sf, M, K, M)
+        return q, sf
+
+    def requant_into(wq, sf, rows, K, group_rows, dst_group_rows, sf_ld, sf_group, seed, chunk_groups=1):
+        """Synthetic checkpoint weights (f32 N(0, 0.02) -> e4m3 + f32 block scales) through glm_requant."""
+        groups = rows // group_rows if group_rows else 1
+        step = chunk_groups
+        for g0 in range(0, max(groups, 1), step):
+            gn = min(step, groups - g0) if groups > 1 else 1
+            r = gn * group_rows if groups > 1 else rows
+            w8, s = synth.weights(r, K, synth.generator(seed + g0, "cuda"), device=dev)
+            wq_off = wq.view(-1)[g0 * dst_group_rows * K:] if groups > 1 else wq
+            sf_off = sf.view(-1)[g0 * sf_group * 4:] if groups > 1 else sf
+            ops.requant(w8, s, wq_off, sf_off, r, K, group_rows if groups > 1 else (rows + 127) // 128 * 128,
+                        dst_group_rows if groups > 1 else 0, 0, sf_ld, sf_group if groups > 1 else 0)
+            del w8, s
+
+    # ---- dense operands
+    for i, (name, n, k, ldc) in enumerate(DENSE):
+        a, sfa = quant_act(k, 100 + i)
+        w = torch.empty(n, k, dtype=torch.uint8, device=dev)
+        sfb = torch.empty(sfw(k) * n * 4, dtype=torch.uint8, device=dev)
+        requant_into(w, sfb, n, k, 0, 0, n, 0, 200 + i)
+        c = torch.empty(M, ldc, dtype=torch.bfloat16, device=dev)
+        data[name] = dict(a=a, sfa=sfa, w=w, sfb=sfb, c=c, n=n, k=k, ldc=ldc)
+
+    # ---- MoE: router -> routing -> psum -> gather (the MoE GEMMs' operands)
+    mcap = TOPK * M + EXPERTS * 128
+    xq, xsf = data["q_a_kv_a"]["a"], data["q_a_kv_a"]["sfa"]      # the normed row's quant (K = 6144)
+    S = synth.router_logits(M, synth.generator(7, "cuda"), device=dev)
+    bias = torch.zeros(EXPERTS, dtype=torch.float32, device=dev)
+    rs = torch.tensor([2.5], dtype=torch.bfloat16, device=dev)
+    ids = torch.empty(M, TOPK, dtype=torch.int32, device=dev)
+    wts = torch.empty(M, TOPK, dtype=torch.float32, device=dev)
+    ops.router_topk(S, bias, rs, ids, wts, M)
+    i32 = lambda *s: torch.empty(*s, dtype=torch.int32, device=dev)
+    moe = dict(ids=ids, wts=wts, counts=i32(ops.counts_len()), cta_batch=i32(mcap // 128), cta_limit=i32(mcap // 128),
+               nne=i32(1), tpad=i32(1), route_map=i32(mcap), exp2perm=i32(M, TOPK), psum=i32(EXPERTS))
+    ops.routing(ids, moe["counts"], moe["cta_batch"], moe["cta_limit"], moe["nne"], moe["tpad"], moe["route_map"],
+                moe["exp2perm"], T=M)
+    ops.moe_psum(moe["counts"], moe["psum"])
+    moe["mq"] = torch.zeros(mcap, H, dtype=torch.uint8, device=dev)
+    moe["msf"] = torch.zeros(sfw(H) * mcap * 4, dtype=torch.uint8, device=dev)
+    ops.moe_gather(xq, xsf, M, moe["exp2perm"], moe["mq"], moe["msf"], mcap, T=M)
+    moe["w13"] = torch.empty(EXPERTS * 2 * INTER, H, dtype=torch.uint8, device=dev)
+    moe["sf13"] = torch.empty(EXPERTS * sfw(H) * 2 * INTER * 4, dtype=torch.uint8, device=dev)
+    requant_into(moe["w13"], moe["sf13"], EXPERTS * 2 * INTER, H, 2 * INTER, 2 * INTER, 2 * INTER,
+                 sfw(H) * 2 * INTER, 300, chunk_groups=16)
+    moe["w2"] = torch.empty(EXPERTS * H, INTER, dtype=torch.uint8, device=dev)
+    moe["sf2"] = torch.empty(EXPERTS * sfw(INTER) * H * 4, dtype=torch.uint8, device=dev)
+    requant_into(moe["w2"], moe["sf2"], EXPERTS * H, INTER, H, H, H, sfw(INTER) * H, 600, chunk_groups=16)
+    moe["mq2"] = torch.zeros(mcap, INTER, dtype=torch.uint8, device=dev)
+    moe["msf2"] = torch.zeros(sfw(INTER) * mcap * 4, dtype=torch.uint8, device=dev)
+    moe["f2"] = torch.zeros(mcap, H, dtype=torch.bfloat16, device=dev)
+    moe["shared"] = torch.zeros(M, H, dtype=torch.bfloat16, device=dev)
+    moe["out"] = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    moe["mcap"] = mcap
+    data["moe"] = moe
+    torch.cuda.synchronize()
+    counts = moe["counts"][:EXPERTS].cpu()
+    moe["R"] = int(counts.sum())
+    moe["blocks"] = int(((counts + 127) // 128).sum())
+    moe["max_count"], moe["min_count"] = int(counts.max()), int(counts.min())
+    return data
+
+
+def launches(data):
+    from kern_glm53_amd import ops
+
+    out = []
+    for name, n, k, ldc in DENSE:
+        t = data[name]
+        out.append((name, 2.0 * M * n * k,
+                    lambda t=t: ops.fp8_gemm(t["a"], t["w"], t["sfa"], t["sfb"], t["c"], M, n=t["n"], k=t["k"],
+                                             rows=M, lda=t["k"], ldc=t["ldc"], sfa_rows=M)))
+    m = data["moe"]
+    R, mcap = m["R"], m["mcap"]
+    out.append(("moe_gate_up_silu_quant", 2.0 * R * 2 * INTER * H,
+                lambda: ops.fp8_gemm_psum_silu_quant(m["mq"], m["w13"], m["msf"], m["sf13"], m["psum"], m["mq2"],
+                                                     m["msf2"], n=2 * INTER, k=H, rows=mcap, lda=H, sfa_rows=mcap,
+                                                     sf_rows=mcap)))
+    out.append(("moe_down", 2.0 * R * H * INTER,
+                lambda: ops.fp8_gemm_psum(m["mq2"], m["w2"], m["msf2"], m["sf2"], m["f2"], m["psum"], n=H, k=INTER,
+                                          rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap)))
+    return out
+
+
+def glue_launches(data):
+    from kern_glm53_amd import ops
+
+    m = data["moe"]
+    xq, xsf = data["q_a_kv_a"]["a"], data["q_a_kv_a"]["sfa"]
+    return [
+        ("routing", lambda: ops.routing(m["ids"], m["counts"], m["cta_batch"], m["cta_limit"], m["nne"], m["tpad"],
+                                        m["route_map"], m["exp2perm"], T=M)),
+        ("moe_psum", lambda: ops.moe_psum(m["counts"], m["psum"])),
+        ("moe_gather", lambda: ops.moe_gather(xq, xsf, M, m["exp2perm"], m["mq"], m["msf"], m["mcap"], T=M)),
+        ("moe_combine", lambda: ops.moe_combine(m["f2"], m["exp2perm"], m["wts"], m["shared"], m["out"], M)),
+    ]
+
+
+def cpu_baseline(data, rows=2048, runs=3):
+    """The oracle's fp32 dequantize-then-matmul (PyTorch-CPU) on rows [0, rows) of each dense GEMM."""
+    from oracle import ref
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    torch.set_num_threads(threads)
+    host = []
+    for name, n, k, _ in DENSE:
+        t = data[name]
+        host.append((t["a"][:rows].cpu().numpy(), t["w"].cpu().numpy(), t["sfa"].cpu().numpy(),
+                     t["sfb"].cpu().numpy(), n, k))
+    flops = sum(2.0 * rows * n * k for *_, n, k in host)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        for a, w, sfa, sfb, n, k in host:
+            ref.fp8_gemm(a, w, sfa, sfb, rows, n, k, k, M)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"rows 0-{rows - 1} of the three dense GEMMs (q_a/kv_a, q_b, o_proj), fp32 dequantize-"
+                      f"then-matmul incl. dequant, median of {runs} runs of {med:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (each GEMM shards trivially by "
+              "rows / experts / heads, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+    log("generating and quantizing synthetic operands on the GPU")
+    data = prepare(dev)
+    m = data["moe"]
+    log(f"routing: R={m['R']} routed rows, {m['blocks']} row blocks, expert rows {m['min_count']}..{m['max_count']}")
+    L = launches(data)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        for _, _, fn in L:
+            fn()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
+
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in L]
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        for i, (_, _, fn) in enumerate(L):
+            ev[s][i][0].record(stream)
+            fn()
+            ev[s][i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    per = {}
+    for i, (name, flops, _) in enumerate(L):
+        ms = statistics.mean(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps))
+        per[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "frac_peak": round(flops / (ms * 1e-3) / PEAK_FP8, 4), "gflop": round(flops / 1e9, 2)}
+    total_flops = sum(f for _, f, _ in L)
+    value = total_flops / (wall / args.steps) / 1e12
+    dom = max(per, key=lambda k: per[k]["ms"])
+    dflops = dict((n, f) for n, f, _ in L)[dom]
+    roofline = {"bound": "mfma", "achieved": round(dflops / (per[dom]["ms"] * 1e-3) / 1e12, 2),
+                "peak": PEAK_FP8 / 1e12, "unit": "TFLOP/s",
+                "frac": round(dflops / (per[dom]["ms"] * 1e-3) / PEAK_FP8, 4), "traffic": None, "kernel": dom}
+    log("per kernel: " + ", ".join(f"{k} {v['ms']:.3f} ms {v['tflops']:.0f} TF/s" for k, v in per.items()))
+
+    # glue around the MoE GEMMs (not part of `value`): mean over a few timed launches
+    glue = {}
+    for name, fn in glue_launches(data):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(5):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        glue[name] = round(e0.elapsed_time(e1) / 5 * 1e3, 1)
+    log("glue (us): " + ", ".join(f"{k} {v}" for k, v in glue.items()))
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle, PyTorch-CPU)")
+        cpu = cpu_baseline(data)
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8_e4m3", "data": "synthetic",
+        "config": {"workload": "GLM-5.3 prefill chunk M=16384: dense fp8 GEMMs q_a/kv_a (N=2624,K=6144), "
+                               "q_b (N=16384,K=2048), o_proj (N=6144,K=16384) + 256-expert top-8 MoE gate_up "
+                               "(N=4096,K=6144, fused SiLU-mul-quant) and down (N=6144,K=2048), Zipf(1.1) routing",
+                   "M": M, "moe_routed_rows": m["R"], "moe_row_blocks": m["blocks"], "frac_peak": round(
+                       value * 1e12 / PEAK_FP8, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": per,
+        "glue_us": glue,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

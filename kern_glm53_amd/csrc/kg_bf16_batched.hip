@@ -1,0 +1,168 @@
+// bf16 GEMM batched over heads (MLA's W_UK absorption and W_UV up-projection) on gfx950:
+// D[r][h][0:n] = bf16(sum_k A[r][h][k] B[h][d][k]), f32 accumulation, every operand a byte-strided view
+// (source/glm_deepgemm.cu:26-33, 42-43; scripts/glm_ops.py:225-236; shapes scripts/gen.py:136-139).
+//
+// HBM-bound (102-169 flop/B against a bf16 ridge of ~315): the design goal is streaming A and D once at
+// full width while the MFMA work hides under it.
+//   * a workgroup = 4 wave64s owns a 128-row x 128-column tile of one head; K advances 64 (128 bytes of a
+//     row) per stage through LDS, copied HBM -> LDS by buffer_load ... lds with the same XOR-swizzled
+//     128-byte rows as the fp8 GEMM; two stages in two distinct LDS arrays;
+//   * v_mfma_f32_32x32x16_bf16 with B (the head's weight rows, n) as the first operand and A (rows r) as
+//     the second, so each lane holds 4 consecutive d of one row: 8-byte stores;
+//   * buffer resources bound every operand, so M / N tails read as zero and need no clamping.
+#include "kg_device.h"
+#include "kg_host.h"
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+#define KG_LDS __attribute__((address_space(3)))
+
+struct KgBf16Args {
+  const u8* a;
+  const u8* b;
+  u8* d;
+  long long a_rs, a_hs, b_rs, b_hs, d_rs, d_hs;
+  int m, n, k, heads, m_tiles, n_tiles;
+};
+
+KG_DEV __amdgpu_buffer_rsrc_t kg_rsrc_b(const void* base, long long bytes) {
+  const int n = bytes > 0x7fffffffll ? 0x7fffffff : (bytes < 0 ? 0 : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+KG_DEV int kg_xcd_remap_b(int bid, int total) {
+  const int per = total >> 3, rem = total & 7, x = bid & 7, local = bid >> 3;
+  return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + local;
+}
+
+KG_DEV v8bf kg_lds_bf16x8(const u8* p) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  v8bf r;
+  __builtin_memcpy(&r, &u, 16);
+  return r;
+}
+
+__global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Args p) {
+  constexpr int BM = 128, BN = 128, TI = 2, TJ = 2, SA = BM * 128, STAGE = (BM + BN) * 128;
+  __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int wid = kg_xcd_remap_b((int)blockIdx.x, (int)gridDim.x);
+  const int per_head = p.m_tiles * p.n_tiles;
+  const int h = wid / per_head, rest = wid - h * per_head;
+  const int mt = rest / p.n_tiles, nt = rest - mt * p.n_tiles;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int mv = min(BM, p.m - m0), nv = min(BN, p.n - n0);
+
+  const __amdgpu_buffer_rsrc_t ra =
+      kg_rsrc_b(p.a + (size_t)h * p.a_hs + (size_t)m0 * p.a_rs, (long long)(mv - 1) * p.a_rs + 2ll * p.k);
+  const __amdgpu_buffer_rsrc_t rb =
+      kg_rsrc_b(p.b + (size_t)h * p.b_hs + (size_t)n0 * p.b_rs, (long long)(nv - 1) * p.b_rs + 2ll * p.k);
+  const int chunk = ((lane & 7) ^ (lane >> 3)) << 4;
+  const unsigned va = (unsigned)((lane >> 3) * p.a_rs + chunk);
+  const unsigned vb = (unsigned)((lane >> 3) * p.b_rs + chunk);
+
+  // fragment offsets: for K step s (16 bf16 = 32 bytes), lane reads chunk 2s + (lane >> 5) of its row
+  const int arow0 = wm * (BM / 2) + (lane & 31), brow0 = wn * (BN / 2) + (lane & 31);
+  unsigned offa[4], offb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const unsigned sw = (unsigned)(((2 * s + (lane >> 5)) ^ (lane & 7)) << 4);
+    offa[s] = (unsigned)arow0 * 128u + sw;
+    offb[s] = (unsigned)SA + (unsigned)brow0 * 128u + sw;
+  }
+
+  v16f acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto issue = [&](u8* stage, int kt) {
+    const int ko = kt * 128;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = (wave * 4 + q) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * 4 + q) * 1024), 16, va,
+                                               (int)(r * p.a_rs) + ko, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * 4 + q) * 1024), 16, vb,
+                                               (int)(r * p.b_rs) + ko, 0, 0);
+    }
+  };
+  auto compute = [&](const u8* stage) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      v8bf af[TI], bf[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) af[i] = kg_lds_bf16x8(stage + offb[s] + i * 32 * 128);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) bf[j] = kg_lds_bf16x8(stage + offa[s] + j * 32 * 128);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int KT = p.k >> 6;
+  issue(st0, 0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    issue(st1, kt + 1);
+    compute(st0);
+    __syncthreads();
+    if (kt + 2 < KT) issue(st0, kt + 2);
+    compute(st1);
+    __syncthreads();
+  }
+  if (kt < KT) compute(st0);
+
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int r = m0 + arow0 + j * 32;
+    if (r >= p.m) continue;
+    u8* drow = p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int dn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
+        const v16f& v = acc[i][j];
+        if (dn + 3 < p.n) {
+          uint2 o;
+          o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(drow + 2 * dn) = o;
+        } else {
+#pragma unroll
+          for (int x = 0; x < 4; ++x)
+            if (dn + x < p.n) reinterpret_cast<u16*>(drow)[dn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
+        }
+      }
+  }
+}
+
+extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
+                               long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
+                               long long d_hs, void* stream) {
+  KG_CHECK(a && b && d && m >= 0 && m <= rows && n > 0 && n % 4 == 0 && k > 0 && k % 64 == 0 && heads > 0);
+  KG_CHECK(a_rs % 16 == 0 && a_hs % 16 == 0 && b_rs % 16 == 0 && b_hs % 16 == 0 && d_rs % 8 == 0 && d_hs % 8 == 0);
+  KG_CHECK(kg_aligned(a, 16) && kg_aligned(b, 16) && kg_aligned(d, 8));
+  KG_CHECK(a_rs >= 2ll * k && b_rs >= 2ll * k && 128ll * a_rs < (1ll << 31) && 128ll * b_rs < (1ll << 31));
+  if (m == 0) return 0;
+  KgBf16Args p{};
+  p.a = (const u8*)a, p.b = (const u8*)b, p.d = (u8*)d;
+  p.a_rs = a_rs, p.a_hs = a_hs, p.b_rs = b_rs, p.b_hs = b_hs, p.d_rs = d_rs, p.d_hs = d_hs;
+  p.m = m, p.n = n, p.k = k, p.heads = heads;
+  p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
+  const long long total = (long long)heads * p.m_tiles * p.n_tiles;
+  KG_CHECK(total < (1ll << 31));
+  hipLaunchKernelGGL(kg_bf16_batched_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}

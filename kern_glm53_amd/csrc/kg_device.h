@@ -1,0 +1,104 @@
+// Device-side helpers shared by every kernel of the library (gfx950 / CDNA4, wave64).
+//
+// Numerics are chosen to be bit-reproducible: bf16 and e4m3 conversions are integer code with
+// round-to-nearest-even (e4m3 saturating to +-448 as CUDA's __NV_SATFINITE in the reference,
+// source/glm_glue.cu:76-79 and source/glm_prep.cu:69), the UE8M0 exponent follows
+// source/glm_glue.cu:67-74, and kg_exp is the path's own exp (Cody-Waite reduction, degree-7 Taylor
+// polynomial, explicit fused multiply-adds) evaluated the same way on every device.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint8_t u8;
+typedef uint16_t u16;
+typedef uint32_t u32;
+typedef uint64_t u64;
+
+#define KG_DEV __device__ __forceinline__
+
+KG_DEV float kg_u2f(u32 u) { return __uint_as_float(u); }
+KG_DEV u32 kg_f2u(float f) { return __float_as_uint(f); }
+
+KG_DEV float kg_bf16_to_f32(u16 h) { return kg_u2f((u32)h << 16); }
+
+// f32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+KG_DEV u16 kg_f32_to_bf16(float f) {
+  u32 u = kg_f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+
+// Two f32 -> packed bf16 pair (lo in bits 0-15).
+KG_DEV u32 kg_pack_bf16x2(float lo, float hi) {
+  return (u32)kg_f32_to_bf16(lo) | ((u32)kg_f32_to_bf16(hi) << 16);
+}
+
+// f32 -> OCP e4m3fn, round to nearest even, saturating to +-448, NaN -> 0x7f | sign.
+KG_DEV u32 kg_e4m3(float x) {
+  const u32 u = kg_f2u(x);
+  const u32 sign = (u >> 24) & 0x80u;
+  const u32 a = u & 0x7fffffffu;
+  u32 r;
+  if (a > 0x7f800000u) {
+    r = 0x7fu;
+  } else if (a >= 0x43e00000u) {
+    r = 0x7eu;
+  } else if (a < 0x3c800000u) {
+    r = (u32)__builtin_rintf(kg_u2f(a) * 512.0f);       // subnormal grid 2^-9, exact scaling
+  } else {
+    r = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - ((127u - 7u) << 3);
+    r = r > 0x7eu ? 0x7eu : r;
+  }
+  return sign | r;
+}
+
+KG_DEV u32 kg_e4m3x4(float a, float b, float c, float d) {
+  return kg_e4m3(a) | (kg_e4m3(b) << 8) | (kg_e4m3(c) << 16) | (kg_e4m3(d) << 24);
+}
+
+// OCP e4m3fn -> f32 (exact).
+KG_DEV float kg_e4m3_to_f32(u32 b) {
+  const u32 s = (b & 0x80u) << 24, e = (b >> 3) & 15u, m = b & 7u;
+  if (e == 15u && m == 7u) return kg_u2f(s | 0x7fc00000u);
+  if (e == 0u) return kg_u2f(s | kg_f2u((float)m * 0.001953125f));       // m * 2^-9
+  return kg_u2f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// UE8M0 block scale of source/glm_glue.cu:67-74: the exponent byte, scale = 2^(e - 127).
+KG_DEV u32 kg_ue8m0(float amax, float eps) {
+  const u32 b = kg_f2u(fmaxf(amax, eps) / 448.0f);   // IEEE division (HIP's default is correctly rounded)
+  return ((b >> 23) & 0xffu) + ((b & 0x7fffffu) != 0u);
+}
+KG_DEV float kg_exp2i(u32 e) { return kg_u2f(e << 23); }
+
+// The path's exp (see the file comment).  Evaluated with explicit fmaf so contraction cannot change it.
+KG_DEV float kg_exp(float x) {
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-04f;
+  p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// SiLU(g) * u rounded to bf16 and back, as source/glm_glue.cu:192 with the path's exp.
+KG_DEV float kg_silu_mul_bf16(float g, float u) {
+  return kg_bf16_to_f32(kg_f32_to_bf16(g / (1.0f + kg_exp(-g)) * u));
+}
+
+// Max over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+KG_DEV float kg_group_max(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}

@@ -1,0 +1,327 @@
+/*
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle: a plain-C, single-threaded restatement of the
+ * byte / integer / order-fixed float arithmetic of kern-glm53's `glm_deepgemm` path glue.  Only the test
+ * suite, the smoke check and the bench's CPU-baseline leg load it, as the checker; the product library
+ * (kern_glm53_amd/csrc) never links, calls or falls back to it.
+ *
+ * Every function cites the reference lines it restates (paths relative to the reference checkout).
+ * Compiled with -ffp-contract=off so that every fused multiply-add below is an explicit fmaf().
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+typedef uint8_t u8;
+typedef uint16_t u16;
+typedef uint32_t u32;
+
+#define KGO_H 6144 /* hidden size the MoE gather / combine are fixed to: source/glm_glue.cu:26 */
+
+/* ---------------------------------------------------------------- scalar conversions */
+
+static inline u32 f2u(float f) { u32 u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(u32 u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* bf16 -> f32 is exact (the upper 16 bits of the f32). */
+float kgo_bf16_to_f32(u16 h) { return u2f((u32)h << 16); }
+
+/* f32 -> bf16, round to nearest even, NaN kept quiet: CUDA __float2bfloat16 (glm_glue.cu:43, 101). */
+u16 kgo_f32_to_bf16(float f) {
+  u32 u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+
+/* OCP e4m3fn -> f32, exact: bias 7, 3 mantissa bits, 0x7f / 0xff are NaN, no infinities. */
+float kgo_e4m3_to_f32(u8 b) {
+  const int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7) return s ? -NAN : NAN;
+  if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf((float)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+/* f32 -> OCP e4m3fn with round-to-nearest-even and saturation to +-448 (CUDA __NV_SATFINITE, as the
+ * __nv_fp8x4_e4m3 constructor of glm_glue.cu:76-79 and __nv_cvt_float_to_fp8 of glm_prep.cu:69). */
+u8 kgo_e4m3_from_f32(float x) {
+  const u32 u = f2u(x);
+  const u8 sign = (u8)((u >> 24) & 0x80u);
+  const u32 a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (u8)(sign | 0x7f);          /* NaN */
+  if (a >= 0x43e00000u) return (u8)(sign | 0x7e);         /* >= 448 (inf included) saturates */
+  if (a < 0x3c800000u) {                                  /* below 2^-6: subnormal grid of 2^-9 */
+    const float q = rintf(u2f(a) * 512.0f);                /* exact scaling, RNE to an integer 0..8 */
+    return (u8)(sign | (u8)q);                             /* 8 is the least normal, code 0x08 */
+  }
+  /* normal: keep 3 of the 23 mantissa bits, ties to even; a carry bumps the exponent */
+  u32 r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
+  r -= (127u - 7u) << 3;
+  if (r > 0x7eu) r = 0x7eu;
+  return (u8)(sign | r);
+}
+
+/* The UE8M0 block scale: glm_glue.cu:67-74 (also glm_prep.cu:57-60).  Returns the exponent byte and
+ * stores 2^(e-127) in *scale. */
+u8 kgo_ue8m0(float amax, float eps, float* scale) {
+  const u32 b = f2u(fmaxf(amax, eps) / 448.0f);
+  u32 x = (b >> 23) & 0xffu;
+  x += (b & 0x7fffffu) != 0;
+  if (scale) *scale = u2f(x << 23);
+  return (u8)x;
+}
+
+/* The path's exp: 2^n * e^r with n = rint(x * log2 e), r = x - n ln2 (Cody-Waite two-constant split,
+ * fused), e^r by its degree-7 Taylor polynomial in Horner form, then ldexp.  The HIP kernels evaluate
+ * the same operations in the same order, so SiLU and the router's sigmoid agree bit for bit. */
+float kgo_exp(float x) {
+  if (x > 88.72283935546875f) return INFINITY;
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412698e-04f;   /* 1/7! */
+  p = fmaf(p, r, 1.38888888888888888889e-03f); /* 1/6! */
+  p = fmaf(p, r, 8.33333333333333333333e-03f); /* 1/5! */
+  p = fmaf(p, r, 4.16666666666666666667e-02f); /* 1/4! */
+  p = fmaf(p, r, 1.66666666666666666667e-01f); /* 1/3! */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* ---------------------------------------------------------------- activation quantization (a1) */
+
+/* One (row, 128-column block) quantized: quant4 over a warp, glm_glue.cu:85-92, with put_sf
+ * glm_glue.cu:81-83.  v holds the block's 128 f32 values. */
+static void quant_block(const float* v, u8* q, u8* sf, int sf_rows, int r, int kb, float eps) {
+  float amax = 0.0f, scale;
+  for (int i = 0; i < 128; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const u8 e = kgo_ue8m0(amax, eps, &scale);
+  const float inv = 1.0f / scale;
+  for (int i = 0; i < 128; ++i) q[i] = kgo_e4m3_from_f32(v[i] * inv);
+  sf[((size_t)(kb >> 2) * sf_rows + r) * 4 + (kb & 3)] = e;
+}
+
+/* glm_quant, glm_glue.cu:164-175: x [T][ldx] bf16 -> q [T][K] e4m3, sf words [ceil(K/512)][sf_rows]. */
+void kgo_quant(const u16* x, int ldx, u8* q, u8* sf, int sf_rows, int K, int T) {
+  float v[128];
+  for (int r = 0; r < T; ++r)
+    for (int kb = 0; kb < K / 128; ++kb) {
+      for (int i = 0; i < 128; ++i) v[i] = kgo_bf16_to_f32(x[(size_t)r * ldx + kb * 128 + i]);
+      quant_block(v, q + (size_t)r * K + kb * 128, sf, sf_rows, r, kb, 1e-10f);
+    }
+}
+
+/* glm_silu_mul_quant, glm_glue.cu:177-194: act = bf16(g / (1 + exp(-g)) * u) over the gate | up halves
+ * of gu [rows][2I], quantized per 128 columns.  Rows at or past *n (when n is given) are skipped. */
+void kgo_silu_mul_quant(const u16* gu, int I, u8* q, u8* sf, int sf_rows, const int* n, int rows) {
+  float v[128];
+  const int live = n ? (*n < rows ? *n : rows) : rows;
+  for (int r = 0; r < live; ++r)
+    for (int kb = 0; kb < I / 128; ++kb) {
+      for (int i = 0; i < 128; ++i) {
+        const float g = kgo_bf16_to_f32(gu[(size_t)r * 2 * I + kb * 128 + i]);
+        const float u = kgo_bf16_to_f32(gu[(size_t)r * 2 * I + I + kb * 128 + i]);
+        v[i] = kgo_bf16_to_f32(kgo_f32_to_bf16(g / (1.0f + kgo_exp(-g)) * u));
+      }
+      quant_block(v, q + (size_t)r * I + kb * 128, sf, sf_rows, r, kb, 1e-10f);
+    }
+}
+
+/* The indexer's per-(row, head) quant of glm_q_post, glm_glue.cu:338-349 (eps 1e-4, values divided by
+ * the power-of-two scale), without the rope: x [rows][heads*128] f32 -> q bytes and the f32 scales. */
+void kgo_head_quant(const float* x, int rows, int heads, u8* q, float* sc) {
+  for (int r = 0; r < rows; ++r)
+    for (int h = 0; h < heads; ++h) {
+      const float* v = x + ((size_t)r * heads + h) * 128;
+      float amax = 0.0f, s;
+      for (int i = 0; i < 128; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      kgo_ue8m0(amax, 1e-4f, &s);
+      for (int i = 0; i < 128; ++i) q[((size_t)r * heads + h) * 128 + i] = kgo_e4m3_from_f32(v[i] / s);
+      sc[(size_t)r * heads + h] = s;
+    }
+}
+
+/* ---------------------------------------------------------------- MoE routing plan (a6, a7) */
+
+/* FlashInfer routingPrecomputed tables over precomputed top-k ids (scripts/glm_ops.py:344-370, the
+ * docstring at 345-347; buffers scripts/gen.py:285-293; the CTA offset convention of
+ * source/glm_glue.cu:446-447).  Within an expert the expanded rows are ranked by ascending expanded
+ * index t * topk + k.  counts has 2 * experts entries: [0, experts) the per-expert row counts, the
+ * upper half zero.  Padding rows of route_map are left untouched. */
+void kgo_moe_routing(const int* ids, int T, int topk, int experts, int tile_log2, int* counts,
+                     int* cta_batch, int* cta_limit, int* num_non_exiting, int* total_padded,
+                     int* route_map, int* exp2perm) {
+  const int tile = 1 << tile_log2;
+  int cnt[1024], off[1024], fill[1024];
+  for (int e = 0; e < experts; ++e) cnt[e] = 0, fill[e] = 0;
+  for (int i = 0; i < T * topk; ++i) {
+    const int e = ids[i];
+    if (e >= 0 && e < experts) ++cnt[e];
+  }
+  int ctas = 0;
+  for (int e = 0; e < experts; ++e) {
+    off[e] = ctas;
+    ctas += (cnt[e] + tile - 1) >> tile_log2;
+  }
+  for (int e = 0; e < experts; ++e) counts[e] = cnt[e], counts[experts + e] = 0;
+  for (int e = 0; e < experts; ++e) {
+    const int nb = (cnt[e] + tile - 1) >> tile_log2;
+    for (int c = 0; c < nb; ++c) {
+      const int lim1 = (off[e] + c + 1) << tile_log2, lim2 = (off[e] << tile_log2) + cnt[e];
+      cta_batch[off[e] + c] = e;
+      cta_limit[off[e] + c] = lim1 < lim2 ? lim1 : lim2;
+    }
+  }
+  *num_non_exiting = ctas;
+  *total_padded = ctas << tile_log2;
+  for (int i = 0; i < T * topk; ++i) {
+    const int e = ids[i];
+    if (e < 0 || e >= experts) { exp2perm[i] = -1; continue; }
+    const int p = (off[e] << tile_log2) + fill[e]++;
+    exp2perm[i] = p;
+    route_map[p] = i / topk;
+  }
+}
+
+/* glm_moe_psum, source/glm_glue.cu:446-461: psum[e] = 128 * (blocks of experts before e) + counts[e]. */
+void kgo_moe_psum(const int* counts, int* psum, int experts) {
+  int incl = 0;
+  for (int e = 0; e < experts; ++e) {
+    const int b = (counts[e] + 127) >> 7;
+    incl += b;
+    psum[e] = (incl - b) * 128 + counts[e];
+  }
+}
+
+/* glm_moe_gather, source/glm_glue.cu:463-475: expanded row (t, k) copied to row exp2perm[t*8+k] of aq,
+ * with its 12 scale words. */
+void kgo_moe_gather(const u8* xq, const u32* xsf, int x_rows, const int* exp2perm, u8* aq, u32* asf, int a_rows,
+                    int T) {
+  for (int e = 0; e < T * 8; ++e) {
+    const int t = e >> 3, p = exp2perm[e];
+    if (p < 0) continue;
+    memcpy(aq + (size_t)p * KGO_H, xq + (size_t)t * KGO_H, KGO_H);
+    for (int w = 0; w < KGO_H / 512; ++w) asf[(size_t)w * a_rows + p] = xsf[(size_t)w * x_rows + t];
+  }
+}
+
+/* glm_moe_combine, source/glm_glue.cu:477-503: out[t] = bf16(shared[t] + sum_k wts[t,k] * fc2[perm]),
+ * the sum an f32 fused multiply-add chain in k order (nvcc contracts acc += w * v). */
+void kgo_moe_combine(const u16* fc2, const int* exp2perm, const float* wts, const u16* shared, u16* out, int T) {
+  for (int t = 0; t < T; ++t)
+    for (int c = 0; c < KGO_H; ++c) {
+      float acc = kgo_bf16_to_f32(shared[(size_t)t * KGO_H + c]);
+      for (int k = 0; k < 8; ++k) {
+        const int p = exp2perm[t * 8 + k];
+        if (p < 0) continue;
+        acc = fmaf(wts[t * 8 + k], kgo_bf16_to_f32(fc2[(size_t)p * KGO_H + c]), acc);
+      }
+      out[(size_t)t * KGO_H + c] = kgo_f32_to_bf16(acc);
+    }
+}
+
+/* ---------------------------------------------------------------- router top-k (a11) */
+
+static inline u32 ord_f32(float f) {
+  const u32 b = f2u(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* kern_k3_router_topk, source/k3/k3_router_argmax.cu:112-176 (math at 28-38): sigmoid, + bias, topk
+ * sequential max picks (ties to the smaller expert, a pick's key dropped to 0), weights sig / (sum +
+ * 1e-20) * f32(rs).  The weight sum follows the 8-lane xor butterfly of 166-171: ((s0+s4)+(s2+s6)) +
+ * ((s1+s5)+(s3+s7)).  The sigmoid uses this oracle's exp (kgo_exp), as the HIP kernel does. */
+void kgo_router_topk(const float* S, const float* bias, const u16* rs, int* idx, float* wts, int B, int experts) {
+  u32 o[1024];
+  float sig[1024];
+  const float rsf = kgo_bf16_to_f32(rs[0]);
+  for (int b = 0; b < B; ++b) {
+    for (int e = 0; e < experts; ++e) {
+      sig[e] = 1.0f / (1.0f + kgo_exp(-S[(size_t)b * experts + e]));
+      o[e] = ord_f32(sig[e] + bias[e]);
+    }
+    int pe[8];
+    float ps[8];
+    for (int r = 0; r < 8; ++r) {
+      int best = 0;
+      for (int e = 1; e < experts; ++e)
+        if (o[e] > o[best]) best = e;
+      pe[r] = best, ps[r] = sig[best];
+      o[best] = 0u;
+    }
+    const float den = ((ps[0] + ps[4]) + (ps[2] + ps[6])) + ((ps[1] + ps[5]) + (ps[3] + ps[7]));
+    for (int r = 0; r < 8; ++r) {
+      wts[b * 8 + r] = (ps[r] / (den + 1e-20f)) * rsf;
+      idx[b * 8 + r] = pe[r];
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- weight layout (a12, a13) */
+
+/* glm_requant, source/glm_prep.cu:30-74: every 128x128 block of e4m3 w with its f32 scale s
+ * re-quantized to a UE8M0 block scale; destination row g * dst_group_rows + dst_row0 + ri for source
+ * row g * group_rows + ri, the exponent byte (kb & 3) of word g * sf_group + (kb >> 2) * sf_ld +
+ * dst_row0 + ri, written for every live row. */
+void kgo_requant(const u8* w, const float* s, u8* wq, u8* sf, int rows, int K, int group_rows, int dst_group_rows,
+                 int dst_row0, int sf_ld, long long sf_group) {
+  static float v[128 * 128];
+  const int nrb = (rows + 127) / 128, nkb = K / 128;
+  for (int rb = 0; rb < nrb; ++rb)
+    for (int kb = 0; kb < nkb; ++kb) {
+      const float scale = s[(size_t)rb * nkb + kb];
+      float amax = 0.0f;
+      for (int i = 0; i < 128; ++i)
+        for (int c = 0; c < 128; ++c) {
+          const int sr = rb * 128 + i;
+          const float x = sr < rows ? kgo_e4m3_to_f32(w[(size_t)sr * K + kb * 128 + c]) * scale : 0.0f;
+          v[i * 128 + c] = x;
+          amax = fmaxf(amax, fabsf(x));
+        }
+      float sc;
+      const u8 e = kgo_ue8m0(amax, 1e-4f, &sc);
+      const float inv = 1.0f / sc;
+      for (int i = 0; i < 128; ++i) {
+        const int sr = rb * 128 + i;
+        if (sr >= rows) break;
+        const int g = sr / group_rows, ri = sr % group_rows;
+        u8* d = wq + ((size_t)g * dst_group_rows + dst_row0 + ri) * K + kb * 128;
+        for (int c = 0; c < 128; ++c) d[c] = kgo_e4m3_from_f32(v[i * 128 + c] * inv);
+        sf[((size_t)g * sf_group + (size_t)(kb >> 2) * sf_ld + dst_row0 + ri) * 4 + (kb & 3)] = e;
+      }
+    }
+}
+
+/* glm_kvb, source/glm_prep.cu:76-85: kv_b [64*448][512] e4m3 with f32 128x128 scales -> bf16 kvb, and
+ * W_UK transposed per head: wuk[h][c][r] = kvb[h*448 + r][c] for r < 192. */
+void kgo_kvb(const u8* w, const float* s, u16* kvb, u16* wuk) {
+  for (int idx = 0; idx < 64 * 448 * 512; ++idx) {
+    const int row = idx >> 9, c = idx & 511;
+    const u16 v = kgo_f32_to_bf16(kgo_e4m3_to_f32(w[idx]) * s[(row >> 7) * 4 + (c >> 7)]);
+    kvb[idx] = v;
+    const int h = row / 448, r = row % 448;
+    if (r < 192) wuk[((size_t)h * 512 + c) * 192 + r] = v;
+  }
+}
+
+/* ---------------------------------------------------------------- array helpers for the Python side */
+
+void kgo_e4m3_encode_n(const float* x, u8* q, long long n) {
+  for (long long i = 0; i < n; ++i) q[i] = kgo_e4m3_from_f32(x[i]);
+}
+void kgo_e4m3_decode_n(const u8* q, float* x, long long n) {
+  for (long long i = 0; i < n; ++i) x[i] = kgo_e4m3_to_f32(q[i]);
+}
+void kgo_exp_n(const float* x, float* y, long long n) {
+  for (long long i = 0; i < n; ++i) y[i] = kgo_exp(x[i]);
+}
+void kgo_ue8m0_n(const float* amax, float eps, u8* e, long long n) {
+  for (long long i = 0; i < n; ++i) e[i] = kgo_ue8m0(amax[i], eps, 0);
+}
+void kgo_bf16_round_n(const float* x, u16* h, long long n) {
+  for (long long i = 0; i < n; ++i) h[i] = kgo_f32_to_bf16(x[i]);
+}

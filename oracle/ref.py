@@ -1,0 +1,381 @@
+"""TEST INFRASTRUCTURE ONLY: the oracle for kern-glm53's `glm_deepgemm` path.
+
+Only the test suite, `__graft_entry__.smoke()` and `bench.py`'s `cpu_baseline` leg import this module, as
+the checker.  The product (`kern_glm53_amd`) never imports, links or falls back to it.
+
+Two halves:
+  * the byte / integer / order-fixed glue restated in plain C (`kg_oracle.c`, built into
+    `_build/libkg_oracle.so` by this directory's Makefile), reached here through ctypes on numpy arrays;
+  * the floating-point GEMM families restated in PyTorch-CPU as fp32 dequantize-then-matmul (the
+    reference's math with exact e4m3 products and power-of-two scales, accumulation order free).
+
+Pinning (what checks this oracle itself) lives in tests/test_oracle.py: the e4m3 codec against torch's
+float8_e4m3fn cast and an exhaustive enumeration, the UE8M0 exponent against a closed form from
+math.frexp, psum against numpy's cumsum, the routing tables against their invariants, the combine's FMA
+chain against exact rational arithmetic, and the GEMM references against brute-force loops and
+single-nonzero probes that fix every scale-layout index.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+import torch
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "libkg_oracle.so"
+
+_lib = None
+
+
+def build() -> pathlib.Path:
+    """Compile the C restatement (make in this directory)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+# ------------------------------------------------------------------ scalar codecs (vectorised through C)
+
+def e4m3_encode(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    q = np.empty(x.shape, dtype=np.uint8)
+    lib().kgo_e4m3_encode_n(_p(x), _p(q), ctypes.c_longlong(x.size))
+    return q
+
+
+def e4m3_decode(q) -> np.ndarray:
+    q = np.ascontiguousarray(np.asarray(q, dtype=np.uint8))
+    x = np.empty(q.shape, dtype=np.float32)
+    lib().kgo_e4m3_decode_n(_p(q), _p(x), ctypes.c_longlong(q.size))
+    return x
+
+
+def exp(x) -> np.ndarray:
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    y = np.empty(x.shape, dtype=np.float32)
+    lib().kgo_exp_n(_p(x), _p(y), ctypes.c_longlong(x.size))
+    return y
+
+
+def ue8m0(amax, eps: float) -> np.ndarray:
+    a = np.ascontiguousarray(np.asarray(amax, dtype=np.float32))
+    e = np.empty(a.shape, dtype=np.uint8)
+    lib().kgo_ue8m0_n(_p(a), ctypes.c_float(eps), _p(e), ctypes.c_longlong(a.size))
+    return e
+
+
+def bf16_round(x) -> np.ndarray:
+    """f32 -> bf16 bits (uint16), round to nearest even."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    h = np.empty(x.shape, dtype=np.uint16)
+    lib().kgo_bf16_round_n(_p(x), _p(h), ctypes.c_longlong(x.size))
+    return h
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.asarray(h, dtype=np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def sf_words(k: int) -> int:
+    """UE8M0 scale words per row: four 128-column blocks a word (scripts/gen.py:72)."""
+    return (k + 511) // 512
+
+
+# ------------------------------------------------------------------ activation quant (a1) and SiLU (a9)
+
+def quant(x_bf16: np.ndarray, K: int, sf_rows: int, T: int | None = None, q=None, sf=None):
+    """glm_quant (source/glm_glue.cu:164-175).  x_bf16 uint16 [T][ldx] -> (q uint8 [T][K],
+    sf uint8 [ceil(K/512) * sf_rows * 4]) with the words laid out [K/512][sf_rows].  q / sf may be given
+    (written in place, untouched bytes kept)."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    T = x.shape[0] if T is None else T
+    ldx = x.shape[1]
+    q = np.zeros((T, K), dtype=np.uint8) if q is None else q
+    sf = np.zeros(sf_words(K) * sf_rows * 4, dtype=np.uint8) if sf is None else sf
+    lib().kgo_quant(_p(x), ctypes.c_int(ldx), _p(q), _p(sf), ctypes.c_int(sf_rows), ctypes.c_int(K), ctypes.c_int(T))
+    return q, sf
+
+
+def silu_mul_quant(gu_bf16: np.ndarray, I: int, sf_rows: int, n: int | None, rows: int, q=None, sf=None):
+    """glm_silu_mul_quant (source/glm_glue.cu:177-194).  Rows >= n are left as given in q / sf."""
+    gu = np.ascontiguousarray(gu_bf16, dtype=np.uint16)
+    q = np.zeros((rows, I), dtype=np.uint8) if q is None else q
+    sf = np.zeros(sf_words(I) * sf_rows * 4, dtype=np.uint8) if sf is None else sf
+    nn = np.array([n if n is not None else 0], dtype=np.int32)
+    lib().kgo_silu_mul_quant(_p(gu), ctypes.c_int(I), _p(q), _p(sf), ctypes.c_int(sf_rows),
+                             _p(nn) if n is not None else None, ctypes.c_int(rows))
+    return q, sf
+
+
+def head_quant(x: np.ndarray):
+    """Per-(row, head) UE8M0 e4m3 quant of 128-wide heads, eps 1e-4 (source/glm_glue.cu:338-342).
+    x f32 [rows][heads][128] -> (q uint8 same shape, scales f32 [rows][heads])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, heads = x.shape[0], x.shape[1]
+    q = np.empty(x.shape, dtype=np.uint8)
+    sc = np.empty((rows, heads), dtype=np.float32)
+    lib().kgo_head_quant(_p(x), ctypes.c_int(rows), ctypes.c_int(heads), _p(q), _p(sc))
+    return q, sc
+
+
+# ------------------------------------------------------------------ MoE routing plan (a6-a8, a10, a11)
+
+def moe_routing(ids: np.ndarray, experts: int = 256, tile_log2: int = 7):
+    """FlashInfer routingPrecomputed tables (scripts/glm_ops.py:344-370) in canonical order."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, topk = ids.shape
+    mcap = topk * T + experts * (1 << tile_log2)
+    counts = np.zeros(2 * experts, dtype=np.int32)
+    ctas = mcap >> tile_log2
+    cta_batch = np.full(ctas, -7, dtype=np.int32)
+    cta_limit = np.full(ctas, -7, dtype=np.int32)
+    nne = np.zeros(1, dtype=np.int32)
+    tpad = np.zeros(1, dtype=np.int32)
+    route_map = np.full(mcap, -7, dtype=np.int32)
+    exp2perm = np.empty((T, topk), dtype=np.int32)
+    lib().kgo_moe_routing(_p(ids), ctypes.c_int(T), ctypes.c_int(topk), ctypes.c_int(experts),
+                          ctypes.c_int(tile_log2), _p(counts), _p(cta_batch), _p(cta_limit), _p(nne), _p(tpad),
+                          _p(route_map), _p(exp2perm))
+    return dict(counts=counts, cta_batch=cta_batch, cta_limit=cta_limit, num_non_exiting=int(nne[0]),
+                total_padded=int(tpad[0]), route_map=route_map, exp2perm=exp2perm)
+
+
+def moe_psum(counts: np.ndarray, experts: int = 256) -> np.ndarray:
+    """glm_moe_psum (source/glm_glue.cu:446-461)."""
+    c = np.ascontiguousarray(counts[:experts], dtype=np.int32)
+    psum = np.empty(experts, dtype=np.int32)
+    lib().kgo_moe_psum(_p(c), _p(psum), ctypes.c_int(experts))
+    return psum
+
+
+def moe_gather(xq, xsf_words, x_rows, exp2perm, a_rows, T, aq=None, asf=None):
+    """glm_moe_gather (source/glm_glue.cu:463-475); xsf / asf as uint32 word arrays [12][rows]."""
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    xsf = np.ascontiguousarray(xsf_words, dtype=np.uint32)
+    e2p = np.ascontiguousarray(exp2perm, dtype=np.int32)
+    aq = np.zeros((a_rows, 6144), dtype=np.uint8) if aq is None else aq
+    asf = np.zeros(12 * a_rows, dtype=np.uint32) if asf is None else asf
+    lib().kgo_moe_gather(_p(xq), _p(xsf), ctypes.c_int(x_rows), _p(e2p), _p(aq), _p(asf), ctypes.c_int(a_rows),
+                         ctypes.c_int(T))
+    return aq, asf
+
+
+def moe_combine(fc2_bf16, exp2perm, wts, shared_bf16, T):
+    """glm_moe_combine (source/glm_glue.cu:477-503), bf16 bits in and out."""
+    fc2 = np.ascontiguousarray(fc2_bf16, dtype=np.uint16)
+    e2p = np.ascontiguousarray(exp2perm, dtype=np.int32)
+    w = np.ascontiguousarray(wts, dtype=np.float32)
+    sh = np.ascontiguousarray(shared_bf16, dtype=np.uint16)
+    out = np.empty((T, 6144), dtype=np.uint16)
+    lib().kgo_moe_combine(_p(fc2), _p(e2p), _p(w), _p(sh), _p(out), ctypes.c_int(T))
+    return out
+
+
+def router_topk(S: np.ndarray, bias: np.ndarray, rs_bf16: int):
+    """kern_k3_router_topk (source/k3/k3_router_argmax.cu:112-176), topk 8."""
+    S = np.ascontiguousarray(S, dtype=np.float32)
+    B, E = S.shape
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    rs = np.array([rs_bf16], dtype=np.uint16)
+    idx = np.empty((B, 8), dtype=np.int32)
+    wts = np.empty((B, 8), dtype=np.float32)
+    lib().kgo_router_topk(_p(S), _p(b), _p(rs), _p(idx), _p(wts), ctypes.c_int(B), ctypes.c_int(E))
+    return idx, wts
+
+
+# ------------------------------------------------------------------ weight layout (a12, a13)
+
+def requant(w8, s, wq, sf, rows, K, group_rows, dst_group_rows=0, dst_row0=0, sf_ld=None, sf_group=0):
+    """glm_requant (source/glm_prep.cu:30-74), in place into wq / sf (uint8 arrays)."""
+    w8 = np.ascontiguousarray(w8, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    lib().kgo_requant(_p(w8), _p(s), _p(wq), _p(sf), ctypes.c_int(rows), ctypes.c_int(K), ctypes.c_int(group_rows),
+                      ctypes.c_int(dst_group_rows), ctypes.c_int(dst_row0),
+                      ctypes.c_int(sf_ld if sf_ld is not None else rows), ctypes.c_longlong(sf_group))
+
+
+def kvb(w8, s):
+    """glm_kvb (source/glm_prep.cu:76-85): bf16 bits kvb [64*448][512], wuk [64][512][192]."""
+    w8 = np.ascontiguousarray(w8, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    kv = np.empty((64 * 448, 512), dtype=np.uint16)
+    wuk = np.empty((64, 512, 192), dtype=np.uint16)
+    lib().kgo_kvb(_p(w8), _p(s), _p(kv), _p(wuk))
+    return kv, wuk
+
+
+# ------------------------------------------------------------------ floating-point GEMM references
+
+_E4M3_LUT = None
+
+
+def _lut() -> torch.Tensor:
+    global _E4M3_LUT
+    if _E4M3_LUT is None:
+        _E4M3_LUT = torch.from_numpy(e4m3_decode(np.arange(256, dtype=np.uint8)))
+    return _E4M3_LUT
+
+
+def decode_e4m3_t(q: torch.Tensor) -> torch.Tensor:
+    """uint8 e4m3 codes -> exact f32 (table lookup)."""
+    return _lut()[q.long()]
+
+
+def scale_exponents(sf_bytes, rows_total: int, k: int, row0: int = 0, nrows: int | None = None,
+                    word_row0: int = 0) -> torch.Tensor:
+    """The per-(row, 128-K-block) UE8M0 exponent bytes of a packed scale buffer: byte (kb & 3) of word
+    (word_row0 + (kb >> 2)) * rows_total + row (scripts/gen.py:72, source/glm_glue.cu:81-83,
+    scripts/glm_ops.py:206-209).  Returns uint8 [nrows][k / 128]."""
+    sf = torch.as_tensor(np.ascontiguousarray(sf_bytes)).view(torch.uint8).reshape(-1)
+    nrows = rows_total - row0 if nrows is None else nrows
+    nkb = k // 128
+    kb = torch.arange(nkb)
+    r = torch.arange(row0, row0 + nrows)
+    idx = ((word_row0 + (kb >> 2))[None, :] * rows_total + r[:, None]) * 4 + (kb & 3)[None, :]
+    return sf[idx]
+
+
+def dequant(q: torch.Tensor, exps: torch.Tensor) -> torch.Tensor:
+    """e4m3 codes [rows][k] with exponent bytes [rows][k/128] -> f32 values x * 2^(e - 127)."""
+    v = decode_e4m3_t(q)
+    sc = torch.pow(2.0, exps.to(torch.float64) - 127.0).to(torch.float32)
+    return v * sc.repeat_interleave(128, dim=1)
+
+
+def fp8_gemm(a, w, sfa, sfb, m, n, k, lda, sfa_rows, dtype=torch.float32) -> torch.Tensor:
+    """DeepGEMM fp8 1d1d Normal (source/glm_deepgemm.cu:38-39; scripts/glm_ops.py:194-215):
+    C[0:m, 0:n] = A[0:m, 0:k] . W[0:n, 0:k]^T with both operands' UE8M0 128-block scales, as an
+    fp32 dequantize-then-matmul (exact products, power-of-two scales).  Returns f32 [m][n]."""
+    A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)[:m, :k]
+    W = torch.as_tensor(np.ascontiguousarray(w)).view(torch.uint8).reshape(-1, k)[:n]
+    ea = scale_exponents(sfa, sfa_rows, k, 0, m)
+    eb = scale_exponents(sfb, n, k, 0, n)
+    return (dequant(A, ea).to(dtype) @ dequant(W, eb).to(dtype).T).to(torch.float32)
+
+
+def fp8_gemm_abs(a, w, sfa, sfb, m, n, k, lda, sfa_rows) -> torch.Tensor:
+    """sum_k |a_k w_k| of the same GEMM: the scale of its f32 accumulation-order noise."""
+    A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)[:m, :k]
+    W = torch.as_tensor(np.ascontiguousarray(w)).view(torch.uint8).reshape(-1, k)[:n]
+    ea = scale_exponents(sfa, sfa_rows, k, 0, m)
+    eb = scale_exponents(sfb, n, k, 0, n)
+    return dequant(A, ea).abs() @ dequant(W, eb).abs().T
+
+
+def psum_ranges(psum: np.ndarray):
+    """Expert g's live rows [round_up128(psum[g-1]), psum[g]) with psum[-1] = 0 (scripts/glm_ops.py:195-198)."""
+    out, prev = [], 0
+    for g, end in enumerate(np.asarray(psum).tolist()):
+        start = (prev + 127) // 128 * 128
+        out.append((start, int(end)))
+        prev = int(end)
+    return out
+
+
+def fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows, abs_too=False):
+    """DeepGEMM fp8 m-grouped psum layout (source/glm_deepgemm.cu:40-41; scripts/glm_ops.py:194-215):
+    for every expert g, its rows of C from its rows of A and its weight rows [g n, (g+1) n) with scale
+    words [g k/512, (g+1) k/512).  Returns (f32 C [rows][n] with NaN on rows no expert owns, abs-sum)."""
+    A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)
+    W = torch.as_tensor(np.ascontiguousarray(w)).view(torch.uint8).reshape(-1, k)
+    C = torch.full((rows, n), float("nan"))
+    S = torch.full((rows, n), float("nan")) if abs_too else None
+    kw = sf_words(k)
+    for g, (s0, s1) in enumerate(psum_ranges(psum)):
+        if s1 <= s0:
+            continue
+        ea = scale_exponents(sfa, sfa_rows, k, s0, s1 - s0)
+        eb = scale_exponents(sfb, n, k, 0, n, word_row0=g * kw)
+        Ad = dequant(A[s0:s1, :k], ea)
+        Wd = dequant(W[g * n:(g + 1) * n], eb)
+        C[s0:s1] = Ad @ Wd.T
+        if abs_too:
+            S[s0:s1] = Ad.abs() @ Wd.abs().T
+    return C, S
+
+
+def bf16_batched(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """DeepGEMM bf16 Batched (source/glm_deepgemm.cu:42-43; scripts/glm_ops.py:225-236): D[r][h][d] =
+    sum_k A[r][h][k] B[h][d][k] with f32 accumulation.  A [rows][heads][k], B [heads][n][k], both bf16
+    tensors (any strides); returns f32 [rows][heads][n]."""
+    a = A.to(torch.float32).permute(1, 0, 2).contiguous()   # [h][r][k]
+    b = B.to(torch.float32).transpose(1, 2).contiguous()    # [h][k][n]
+    return torch.bmm(a, b).permute(1, 0, 2).contiguous()
+
+
+def mqa_logits(q8, k8, ksf, w, ks, ke, num_q, stride):
+    """DeepGEMM fp8 MQA logits (source/glm_deepgemm.cu:44-45; scripts/glm_ops.py:239-268): for row r < num_q
+    and j < ke[r] - ks[r], logits[r][j] = sum_h w[r][h] * relu(ksf[ks[r]+j] * (q[r][h] . k[ks[r]+j])),
+    evaluated in f64 from exact e4m3 values.  Entries at or past ke - ks are NaN (unspecified)."""
+    qd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(q8)).view(torch.uint8)).to(torch.float64)
+    kd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(k8)).view(torch.uint8)).to(torch.float64)
+    ksf = torch.as_tensor(np.asarray(ksf, dtype=np.float32)).to(torch.float64)
+    w = torch.as_tensor(np.asarray(w, dtype=np.float32)).to(torch.float64)
+    out = torch.full((num_q, stride), float("nan"), dtype=torch.float64)
+    for r in range(num_q):
+        a, b = int(ks[r]), int(ke[r])
+        if b <= a:
+            continue
+        s = (qd[r] @ kd[a:b].T) * ksf[a:b][None, :]          # [heads][klen]
+        out[r, :b - a] = (w[r][:, None] * torch.relu(s)).sum(0)
+    return out
+
+
+def mqa_logits_abs(q8, k8, ksf, w, ks, ke, num_q, stride):
+    """sum_h |w| * ksf * sum_d |q k| : the scale of the f32 evaluation noise of mqa_logits."""
+    qd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(q8)).view(torch.uint8)).to(torch.float64).abs()
+    kd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(k8)).view(torch.uint8)).to(torch.float64).abs()
+    ksf = torch.as_tensor(np.asarray(ksf, dtype=np.float32)).to(torch.float64)
+    w = torch.as_tensor(np.asarray(w, dtype=np.float32)).to(torch.float64).abs()
+    out = torch.zeros((num_q, stride), dtype=torch.float64)
+    for r in range(num_q):
+        a, b = int(ks[r]), int(ke[r])
+        if b <= a:
+            continue
+        out[r, :b - a] = (w[r][:, None] * (qd[r] @ kd[a:b].T) * ksf[a:b][None, :]).sum(0)
+    return out
+
+
+# ------------------------------------------------------------------ tolerance helpers
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """The bf16 unit in the last place at |x| (normal range; 2^-133 floor for zero / subnormal)."""
+    ax = x.abs().to(torch.float64).clamp_min(2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(ax)) - 7)
+
+
+def to_bf16_f32(x: torch.Tensor) -> torch.Tensor:
+    """Round an f32 tensor to bf16 (RNE) and back."""
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def check_bf16_gemm(out_bf16: torch.Tensor, ref32: torch.Tensor, abs_sum: torch.Tensor, k: int, ulps: float = 2.0,
+                    steps_per_mfma: int = 64):
+    """The GEMM output bar: rel-L2 <= 1e-3 and max |out - bf16(ref)| <= ulps bf16 ulp, plus the f32
+    accumulation-order noise bound (k / steps_per_mfma + 32) * 2^-24 * sum|a w| for rows that cancel.
+    Returns (ok, rel_l2, worst_ratio)."""
+    out = out_bf16.to(torch.float64)
+    ref = to_bf16_f32(ref32).to(torch.float64)
+    rel = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+    tol = ulps * bf16_ulp(ref) + (k / steps_per_mfma + 32) * 2.0 ** -24 * abs_sum.to(torch.float64)
+    ratio = float(((out - ref).abs() / tol).max()) if out.numel() else 0.0
+    return rel <= 1e-3 and ratio <= 1.0, rel, ratio

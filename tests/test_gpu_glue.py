@@ -1,0 +1,234 @@
+"""GPU parity of the byte / integer glue against the oracle: bit-exact on the same seeded inputs, including
+the edge cases the reference's kernels guard (rows past a live count, dropped expanded rows, empty and
+1-3-block experts, strided inputs), plus size-independent properties at the full benchmark sizes."""
+import numpy as np
+import pytest
+import torch
+
+from kern_glm53_amd import ops, synth
+from oracle import ref
+from tests._gpu import DEV, bf16_bits, d, filled, h
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_host(M, K, seed, **kw):
+    return bf16_bits(synth.activations(M, K, synth.generator(seed), **kw))
+
+
+# ------------------------------------------------------------------ quant (a1)
+
+@pytest.mark.parametrize("T,K,ldx,sf_rows", [(64, 6144, 6144, 80), (5, 512, 520, 7), (1, 128, 128, 1),
+                                             (33, 2048, 2048, 33), (17, 16384, 16384, 24)])
+def test_quant_bit_exact(T, K, ldx, sf_rows):
+    x = np.zeros((T, ldx), np.uint16)
+    x[:, :K] = bf16_host(T, K, seed=T + K)
+    x[0, :128] = 0                                    # an all-zero block (eps decides the scale)
+    q_ref = np.full((T, K), 0x5a, np.uint8)
+    sf_ref = np.full(ref.sf_words(K) * sf_rows * 4, 0xa5, np.uint8)
+    ref.quant(x, K, sf_rows, T, q_ref, sf_ref)
+    q = filled((T, K), 0x5a)
+    sf = filled((ref.sf_words(K) * sf_rows * 4,), 0xa5)
+    ops.quant(d(x), ldx, q, sf, sf_rows, K, T)
+    assert np.array_equal(h(q, np.uint8), q_ref)
+    assert np.array_equal(h(sf, np.uint8), sf_ref)
+
+
+def test_quant_full_size_properties():
+    """16384 x 6144 (the dense GEMMs' activation): every (row, block) satisfies the UE8M0 contract and
+    matches the oracle on a sample of rows."""
+    T, K = 16384, 6144
+    x = synth.activations(T, K, synth.generator(3, "cuda"), device="cuda")
+    q = torch.empty(T, K, dtype=torch.uint8, device=DEV)
+    sf = torch.empty(ref.sf_words(K) * T * 4, dtype=torch.uint8, device=DEV)
+    ops.quant(x, K, q, sf, T, K, T)
+    rows = torch.randint(0, T, (96,), generator=synth.generator(4)).tolist()
+    xs = bf16_bits(x[rows])
+    q_ref, sf_ref = ref.quant(xs, K, len(rows))
+    assert np.array_equal(h(q[rows], np.uint8), q_ref)
+    e = ref.scale_exponents(h(sf, np.uint8), T, K)
+    e_ref = ref.scale_exponents(sf_ref, len(rows), K)
+    assert torch.equal(e[rows], e_ref)
+    # contract on every block: |dequant - x| <= half an e4m3 step, and the scale is the least power of 2
+    deq = ref.dequant(q.cpu(), e).view(T, K // 128, 128)
+    xf = x.float().cpu().view(T, K // 128, 128)
+    amax = xf.abs().amax(-1)
+    sc = torch.pow(2.0, e.double() - 127).float()
+    assert torch.all(amax / sc <= 448 * (1 + 2.0 ** -20))
+    assert torch.all((amax / (sc / 2) > 448 * (1 - 2.0 ** -20)) | (amax <= 1e-10))
+    # round to nearest: half a step, 2^-4 relative for normals, 2^-10 of the scale for subnormals
+    assert torch.all((deq - xf).abs() <= torch.maximum(xf.abs() * 2.0 ** -4, sc[..., None] * 2.0 ** -10))
+
+
+# ------------------------------------------------------------------ SiLU-mul-quant (a9)
+
+@pytest.mark.parametrize("rows,I,n,sf_rows", [(100, 2048, 70, 128), (64, 256, None, 64), (3, 12288, 2, 8)])
+def test_silu_mul_quant_bit_exact(rows, I, n, sf_rows):
+    g = synth.generator(rows + I)
+    gu = bf16_bits((torch.randn(rows, 2 * I, generator=g) * 3).to(torch.bfloat16))
+    q_ref = np.full((rows, I), 0x33, np.uint8)
+    sf_ref = np.full(ref.sf_words(I) * sf_rows * 4, 0x44, np.uint8)
+    ref.silu_mul_quant(gu, I, sf_rows, n, rows, q_ref, sf_ref)
+    q = filled((rows, I), 0x33)
+    sf = filled((ref.sf_words(I) * sf_rows * 4,), 0x44)
+    nn = torch.tensor([n], dtype=torch.int32, device=DEV) if n is not None else None
+    ops.silu_mul_quant(d(gu), I, q, sf, sf_rows, nn, rows)
+    assert np.array_equal(h(q, np.uint8), q_ref)
+    assert np.array_equal(h(sf, np.uint8), sf_ref)
+
+
+# ------------------------------------------------------------------ routing, psum (a6, a7)
+
+def zipf_ids(T, seed):
+    S = synth.router_logits(T, synth.generator(seed))
+    return torch.topk(S, 8, dim=1).indices.to(torch.int32).numpy()
+
+
+def edge_ids():
+    counts = [0, 1, 127, 128, 129, 256, 255, 383, 2, 0, 64]
+    T = 512
+    rest = T * 8 - sum(counts)
+    per = rest // (256 - len(counts))
+    counts += [per] * (256 - len(counts))
+    counts[len(counts) - 1] += T * 8 - sum(counts)
+    return synth.forced_counts_ids(counts, T, gen=synth.generator(5)).numpy()
+
+
+def run_routing(ids):
+    T = ids.shape[0]
+    mcap = 8 * T + 256 * 128
+    ctas = mcap // 128
+    counts = filled((512,), -3, torch.int32)
+    cta_batch = filled((ctas,), -7, torch.int32)
+    cta_limit = filled((ctas,), -7, torch.int32)
+    nne = filled((1,), -1, torch.int32)
+    tpad = filled((1,), -1, torch.int32)
+    route_map = filled((mcap,), -7, torch.int32)
+    e2p = filled((T, 8), -9, torch.int32)
+    ops.routing(d(ids), counts, cta_batch, cta_limit, nne, tpad, route_map, e2p, T=T)
+    return dict(counts=h(counts, np.int32), cta_batch=h(cta_batch, np.int32), cta_limit=h(cta_limit, np.int32),
+                num_non_exiting=int(h(nne, np.int32)[0]), total_padded=int(h(tpad, np.int32)[0]),
+                route_map=h(route_map, np.int32), exp2perm=h(e2p, np.int32))
+
+
+@pytest.mark.parametrize("kind", ["edge", "zipf-2048", "zipf-16384", "one-token"])
+def test_routing_tables_bit_exact(kind):
+    ids = {"edge": edge_ids, "zipf-2048": lambda: zipf_ids(2048, 6), "zipf-16384": lambda: zipf_ids(16384, 7),
+           "one-token": lambda: np.arange(8, dtype=np.int32)[None, :]}[kind]()
+    got = run_routing(ids)
+    want = ref.moe_routing(ids)
+    nne = want["num_non_exiting"]
+    assert got["num_non_exiting"] == nne and got["total_padded"] == want["total_padded"]
+    assert np.array_equal(got["counts"], want["counts"])
+    assert np.array_equal(got["cta_batch"][:nne], want["cta_batch"][:nne])
+    assert np.array_equal(got["cta_limit"][:nne], want["cta_limit"][:nne])
+    assert np.array_equal(got["exp2perm"], want["exp2perm"])
+    live = want["route_map"] != -7
+    assert np.array_equal(got["route_map"][live], want["route_map"][live])
+    assert np.all(got["route_map"][~live] == -7)              # padding rows untouched
+    psum = torch.empty(256, dtype=torch.int32, device=DEV)
+    ops.moe_psum(d(got["counts"]), psum)
+    assert np.array_equal(h(psum, np.int32), ref.moe_psum(want["counts"]))
+
+
+# ------------------------------------------------------------------ gather, combine (a8, a10)
+
+def test_gather_bit_exact():
+    T = 300
+    ids = zipf_ids(T, 8)
+    tab = ref.moe_routing(ids)
+    e2p = tab["exp2perm"].copy()
+    e2p[7, 3] = -1
+    rng = np.random.default_rng(9)
+    xq = rng.integers(0, 256, (T, 6144), dtype=np.uint8)
+    x_rows = T + 20
+    xsf = rng.integers(0, 1 << 32, 12 * x_rows, dtype=np.uint32)
+    a_rows = 8 * T + 256 * 128
+    aq_ref = np.full((a_rows, 6144), 0x11, np.uint8)
+    asf_ref = np.full(12 * a_rows, 0x22222222, np.uint32)
+    ref.moe_gather(xq, xsf, x_rows, e2p, a_rows, T, aq_ref, asf_ref)
+    aq = filled((a_rows, 6144), 0x11)
+    asf = filled((12 * a_rows,), 0x22222222, torch.int32)
+    ops.moe_gather(d(xq), d(xsf), x_rows, d(e2p), aq, asf, a_rows, T=T)
+    assert np.array_equal(h(aq, np.uint8), aq_ref)
+    assert np.array_equal(h(asf, np.uint32), asf_ref)
+
+
+def test_combine_bit_exact():
+    T = 200
+    ids = zipf_ids(T, 10)
+    tab = ref.moe_routing(ids)
+    e2p = tab["exp2perm"].copy()
+    e2p[5, 0] = -1
+    rows = tab["total_padded"]
+    g = synth.generator(11)
+    fc2 = bf16_bits(torch.randn(rows, 6144, generator=g).to(torch.bfloat16))
+    shared = bf16_bits(torch.randn(T, 6144, generator=g).to(torch.bfloat16))
+    wts = torch.rand(T, 8, generator=g).numpy().astype(np.float32)
+    want = ref.moe_combine(fc2, e2p, wts, shared, T)
+    out = filled((T, 6144), 0, torch.int16)
+    ops.moe_combine(d(fc2), d(e2p), d(wts), d(shared), out, T)
+    assert np.array_equal(h(out, np.uint16), want)
+
+
+# ------------------------------------------------------------------ router (a11)
+
+def test_router_topk_bit_exact():
+    B = 1000
+    S = synth.router_logits(B, synth.generator(12)).numpy()
+    S[0, 10] = S[0, 20] = 40.0
+    bias = (np.random.default_rng(13).standard_normal(256) * 0.05).astype(np.float32)
+    bias[10] = bias[20] = 1.0
+    rs = ref.bf16_round(np.float32([2.5]))
+    idx_ref, wts_ref = ref.router_topk(S, bias, int(rs[0]))
+    idx = torch.empty(B, 8, dtype=torch.int32, device=DEV)
+    wts = torch.empty(B, 8, dtype=torch.float32, device=DEV)
+    ops.router_topk(d(S), d(bias), d(rs), idx, wts, B)
+    assert np.array_equal(h(idx, np.int32), idx_ref)
+    assert np.array_equal(h(wts, np.float32), wts_ref)
+
+
+# ------------------------------------------------------------------ weight layout (a12, a13)
+
+def test_requant_bit_exact():
+    g = synth.generator(14)
+    groups, gr, K = 4, 256, 1024
+    w8, s = synth.weights(groups * gr, K, g)
+    w8, s = w8.numpy(), s.numpy()
+    dst_group_rows, row0 = 2 * gr, gr
+    sf_group = ref.sf_words(K) * dst_group_rows
+    wq_ref = np.full((groups * dst_group_rows, K), 0x66, np.uint8)
+    sf_ref = np.full(groups * sf_group * 4, 0x77, np.uint8)
+    ref.requant(w8, s, wq_ref, sf_ref, groups * gr, K, gr, dst_group_rows, row0, dst_group_rows, sf_group)
+    wq = filled(wq_ref.shape, 0x66)
+    sf = filled(sf_ref.shape, 0x77)
+    ops.requant(d(w8), d(s), wq, sf, groups * gr, K, gr, dst_group_rows, row0, dst_group_rows, sf_group)
+    assert np.array_equal(h(wq, np.uint8), wq_ref)
+    assert np.array_equal(h(sf, np.uint8), sf_ref)
+
+
+def test_requant_ragged_rows():
+    g = synth.generator(15)
+    rows, K = 300, 512
+    w8, s = synth.weights(rows, K, g)
+    w8, s = w8.numpy(), s.numpy()
+    wq_ref = np.zeros((rows, K), np.uint8)
+    sf_ref = np.zeros(ref.sf_words(K) * rows * 4, np.uint8)
+    ref.requant(w8, s, wq_ref, sf_ref, rows, K, 384, 0, 0, rows, 0)
+    wq = filled(wq_ref.shape, 0)
+    sf = filled(sf_ref.shape, 0)
+    ops.requant(d(w8), d(s), wq, sf, rows, K, 384, 0, 0, rows, 0)
+    assert np.array_equal(h(wq, np.uint8), wq_ref) and np.array_equal(h(sf, np.uint8), sf_ref)
+
+
+def test_kvb_bit_exact():
+    rng = np.random.default_rng(16)
+    w8 = rng.integers(0, 256, (64 * 448, 512), dtype=np.uint8)
+    w8[(w8 & 0x7f) == 0x7f] = 0
+    s = np.exp2(rng.uniform(-10, -2, (224, 4))).astype(np.float32)
+    kv_ref, wuk_ref = ref.kvb(w8, s)
+    kv = filled((64 * 448, 512), 0, torch.int16)
+    wuk = filled((64, 512, 192), 0, torch.int16)
+    ops.kvb(d(w8), d(s), kv, wuk)
+    assert np.array_equal(h(kv, np.uint16), kv_ref)
+    assert np.array_equal(h(wuk, np.uint16), wuk_ref)
