@@ -122,6 +122,7 @@ __global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Arg
     __syncthreads();
   }
   if (kt < KT) compute(st0);
+  kg_mfma_drain();
 
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {

@@ -95,6 +95,17 @@ KG_DEV float kg_silu_mul_bf16(float g, float u) {
   return kg_bf16_to_f32(kg_f32_to_bf16(g / (1.0f + kg_exp(-g)) * u));
 }
 
+// Drains the matrix pipe before an epilogue: no instruction may be scheduled across this point, and
+// 64 wait states cover a full 16-pass v_mfma_scale_f32_32x32x64_f8f6f4.  Without it the compiler may
+// interleave the first epilogue instructions (v_accvgpr_read into VGPRs freed by register allocation)
+// with the last MFMAs still reading those VGPRs as operands; measured on gfx950 as ~3% of fused-epilogue
+// outputs one e4m3 code off, gone with the fence.
+KG_DEV void kg_mfma_drain() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Max over groups of `width` consecutive lanes (width a power of two <= 64).
 template <int WIDTH>
 KG_DEV float kg_group_max(float v) {

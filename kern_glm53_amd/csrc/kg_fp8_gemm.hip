@@ -230,6 +230,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   }
 
   // ---- epilogue
+  kg_mfma_drain();
   if constexpr (MODE != 2) {
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {

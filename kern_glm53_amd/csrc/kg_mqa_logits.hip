@@ -106,6 +106,10 @@ __global__ __launch_bounds__(256, 2) void kg_mqa_logits_kernel(const u8* __restr
         acc[t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qf[kh], kf, acc[t], 0, 0, 0, 127, 0, 127);
       }
     }
+    // keep the epilogue's register writes clear of the operands of MFMAs still in the pipe
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n s_nop 7" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       float s = 0.0f;

@@ -281,6 +281,25 @@ def fp8_gemm_abs(a, w, sfa, sfb, m, n, k, lda, sfa_rows) -> torch.Tensor:
     return dequant(A, ea).abs() @ dequant(W, eb).abs().T
 
 
+def _group_max(x: torch.Tensor, group: int = 64) -> torch.Tensor:
+    """max |x| over consecutive groups of `group` columns: [rows][k] -> [rows][k / group]."""
+    r, k = x.shape
+    return x.abs().view(r, k // group, group).amax(-1)
+
+
+def fp8_window_bound(a, w, sfa, sfb, m, n, k, lda, sfa_rows, row0=0, w_row0=0, sfb_word_row0=0) -> torch.Tensor:
+    """sum over 64-wide K groups of max|a| * max|w| (dequantized), per output [m][n]: the scale of the fp8
+    MFMA's in-instruction rounding.  gfx950's v_mfma_scale_f32_32x32x64_f8f6f4 sums an instruction's 64
+    products in a fixed-point window that keeps bits down to 2^-13 of the largest product (measured:
+    1 + 2^-13 is exact, 1 + 2^-14 returns 1; the accumulator C is added in f32), so one instruction's error
+    is below 64 * 2^-13 * max|p| <= 2^-7 * max|a| max|w| over its 64 products."""
+    A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)[row0:row0 + m, :k]
+    W = torch.as_tensor(np.ascontiguousarray(w)).view(torch.uint8).reshape(-1, k)[w_row0:w_row0 + n]
+    ea = scale_exponents(sfa, sfa_rows, k, row0, m)
+    eb = scale_exponents(sfb, n, k, 0, n, word_row0=sfb_word_row0)
+    return _group_max(dequant(A, ea)).double() @ _group_max(dequant(W, eb)).double().T
+
+
 def psum_ranges(psum: np.ndarray):
     """Expert g's live rows [round_up128(psum[g-1]), psum[g]) with psum[-1] = 0 (scripts/glm_ops.py:195-198)."""
     out, prev = [], 0
@@ -289,6 +308,17 @@ def psum_ranges(psum: np.ndarray):
         out.append((start, int(end)))
         prev = int(end)
     return out
+
+
+def fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows):
+    """fp8_window_bound of the m-grouped GEMM, per expert's live rows (NaN elsewhere)."""
+    Wb = torch.full((rows, n), float("nan"), dtype=torch.float64)
+    kw = sf_words(k)
+    for g, (s0, s1) in enumerate(psum_ranges(psum)):
+        if s1 > s0:
+            Wb[s0:s1] = fp8_window_bound(a, w, sfa, sfb, s1 - s0, n, k, lda, sfa_rows, row0=s0, w_row0=g * n,
+                                         sfb_word_row0=g * kw)
+    return Wb
 
 
 def fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows, abs_too=False):
@@ -355,6 +385,23 @@ def mqa_logits_abs(q8, k8, ksf, w, ks, ke, num_q, stride):
     return out
 
 
+def mqa_logits_window(q8, k8, ksf, w, ks, ke, num_q, stride):
+    """fp8 MFMA window scale of mqa_logits: sum_h |w| ksf sum_{2 groups of 64 d} max|q| max|k|."""
+    qd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(q8)).view(torch.uint8)).to(torch.float64).abs()
+    kd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(k8)).view(torch.uint8)).to(torch.float64).abs()
+    qg = qd.view(qd.shape[0], qd.shape[1], 2, 64).amax(-1)               # [q][h][2]
+    kg = kd.view(kd.shape[0], 2, 64).amax(-1)                            # [kv][2]
+    ksf = torch.as_tensor(np.asarray(ksf, dtype=np.float32)).to(torch.float64)
+    w = torch.as_tensor(np.asarray(w, dtype=np.float32)).to(torch.float64).abs()
+    out = torch.zeros((num_q, stride), dtype=torch.float64)
+    for r in range(num_q):
+        a, b = int(ks[r]), int(ke[r])
+        if b <= a:
+            continue
+        out[r, :b - a] = (w[r][:, None] * (qg[r] @ kg[a:b].T) * ksf[a:b][None, :]).sum(0)
+    return out
+
+
 # ------------------------------------------------------------------ tolerance helpers
 
 def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
@@ -369,13 +416,16 @@ def to_bf16_f32(x: torch.Tensor) -> torch.Tensor:
 
 
 def check_bf16_gemm(out_bf16: torch.Tensor, ref32: torch.Tensor, abs_sum: torch.Tensor, k: int, ulps: float = 2.0,
-                    steps_per_mfma: int = 64):
+                    steps_per_mfma: int = 64, window: torch.Tensor | None = None):
     """The GEMM output bar: rel-L2 <= 1e-3 and max |out - bf16(ref)| <= ulps bf16 ulp, plus the f32
-    accumulation-order noise bound (k / steps_per_mfma + 32) * 2^-24 * sum|a w| for rows that cancel.
+    accumulation-order noise bound (k / steps_per_mfma + 32) * 2^-24 * sum|a w| for rows that cancel, plus
+    (fp8 MFMA) 2^-7 * window, window = fp8_window_bound(...) (the hardware's in-instruction rounding).
     Returns (ok, rel_l2, worst_ratio)."""
     out = out_bf16.to(torch.float64)
     ref = to_bf16_f32(ref32).to(torch.float64)
     rel = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
     tol = ulps * bf16_ulp(ref) + (k / steps_per_mfma + 32) * 2.0 ** -24 * abs_sum.to(torch.float64)
+    if window is not None:
+        tol = tol + 2.0 ** -7 * window.to(torch.float64)
     ratio = float(((out - ref).abs() / tol).max()) if out.numel() else 0.0
     return rel <= 1e-3 and ratio <= 1.0, rel, ratio

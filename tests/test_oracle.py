@@ -492,3 +492,21 @@ def test_bf16_batched_reference():
             for d in range(7):
                 want = float((A[r, h].double() * B[h, d].double()).sum())
                 assert abs(float(D[r, h, d]) - want) <= 1e-5 * (1 + abs(want))
+
+
+def test_fp8_window_bound_brute_force():
+    """The window bound equals sum over 64-wide K groups of max|a| * max|w| (dequantized), by loops."""
+    rng = np.random.default_rng(19)
+    M, N, K = 3, 4, 256
+    a = rng.integers(0, 0x70, (M, K), dtype=np.uint8) | (rng.integers(0, 2, (M, K)) << 7).astype(np.uint8)
+    w = rng.integers(0, 0x70, (N, K), dtype=np.uint8)
+    ea = rng.integers(120, 130, (M, K // 128)).astype(np.uint8)
+    eb = rng.integers(120, 130, (N, K // 128)).astype(np.uint8)
+    B = ref.fp8_window_bound(a, w, pack_exps(ea, M, K), pack_exps(eb, N, K), M, N, K, K, M).numpy()
+    da = ref.e4m3_decode(a).astype(np.float64) * np.exp2(np.repeat(ea.astype(np.float64) - 127, 128, 1))
+    dw = ref.e4m3_decode(w).astype(np.float64) * np.exp2(np.repeat(eb.astype(np.float64) - 127, 128, 1))
+    for m in range(M):
+        for n in range(N):
+            want = sum(np.abs(da[m, g * 64:(g + 1) * 64]).max() * np.abs(dw[n, g * 64:(g + 1) * 64]).max()
+                       for g in range(K // 64))
+            assert abs(B[m, n] - want) <= 1e-12 * want
