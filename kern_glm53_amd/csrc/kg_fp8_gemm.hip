@@ -85,6 +85,18 @@ KG_DEV void kg_fp8_issue(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgp
                                              woff[q] + ko, 0, 0);
 }
 
+// DMA instruction q of one K block for this wave: q < NQA an A chunk, else a W chunk.
+template <int NQA, int NQB, int SA>
+KG_DEV void kg_fp8_dma(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw, unsigned va,
+                       unsigned vw, int lda, const int* woff, int ko, int q) {
+  if (q < NQA)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16, va,
+                                             (wave * NQA + q) * 8 * lda + ko, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q - NQA) * 1024), 16,
+                                             vw, woff[q - NQA] + ko, 0, 0);
+}
+
 template <int BM, int BN, int MODE>
 __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) {
   constexpr int TJ = BM / 64;            // m tiles (32 rows) per wave  -> MFMA operand B
@@ -175,59 +187,114 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 #pragma unroll
   for (int q = 0; q < NQB; ++q) woff[q] = kg_wrow<MODE, BN>(n0, half, (wave * NQB + q) * 8) * p.k;
 
-  auto issue = [&](u8* stage, int kt) { kg_fp8_issue<NQA, NQB, SA>(stage, wave, ra, rw, va, vw, p.lda, woff, kt * 128); };
-
+  // ---- software-pipelined main loop (one K block of 128 per step, two LDS stages).
+  // The MFMAs of a K half run as NO rows x NI columns: the "inner" operand's NI fragments stay in
+  // registers for the whole half (double-buffered across halves), the "outer" operand's fragment of the
+  // next row is read while the current row's MFMAs issue (2-deep ping-pong).  The outer operand is the one
+  // with fewer tiles.  In the second half the last read of the current stage CUR is issued NI MFMAs before
+  // the workgroup barrier; after it (every wave's DMA into NXT has landed, every wave is done with CUR)
+  // come the next step's first-half reads from NXT and the DMA of K block kt + 2 into CUR.
+  // sched_barrier(0) after every MFMA pins the order, so the matrix pipe always has work queued.
+  constexpr bool OUTER_W = TI <= TJ;          // which operand is streamed row by row
+  constexpr int NO = OUTER_W ? TI : TJ, NI = OUTER_W ? TJ : TI;
+  constexpr int NM = NO * NI;
+  static_assert(NO % 2 == 0 && NO >= 2, "the outer ping-pong needs an even row count");
+  constexpr int BAR = (NO - 2) * NI + 1;      // second-half MFMA after which the barrier sits
+  constexpr int NSLOT = NM - 1 - BAR;         // second-half slots after the barrier
+  v8i res[2][NI], str[2];
   u32 wa[TJ], wb[TI];
-  auto load_words = [&](int kt) {
-    const int kg4 = kt >> 2;
-#pragma unroll
-    for (int j = 0; j < TJ; ++j)
-      wa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, kg4 * p.sfa_rows * 4, 0);
-#pragma unroll
-    for (int i = 0; i < TI; ++i) wb[i] = __builtin_amdgcn_raw_buffer_load_b32(rsb, sb_off[i], kg4 * p.n * 4, 0);
-  };
+#define KG_LOAD_WORDS(KTV, XA, XB)                                                                         \
+  do {                                                                                                    \
+    const int kg4_ = (KTV) >> 2;                                                                           \
+    _Pragma("unroll") for (int j = 0; j < TJ; ++j)                                                         \
+      XA[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, kg4_ * p.sfa_rows * 4, 0);        \
+    _Pragma("unroll") for (int i = 0; i < TI; ++i)                                                         \
+      XB[i] = __builtin_amdgcn_raw_buffer_load_b32(rsb, sb_off[i], kg4_ * p.n * 4, 0);                      \
+  } while (0)
+  // fragment of operand row x (outer if O, else inner) of K half kh from a stage
+#define KG_FRAG_W(ST, KH, I) kg_lds_frag((ST) + wtile(I) * 128, offw[KH][0], offw[KH][1])
+#define KG_FRAG_A(ST, KH, J) kg_lds_frag((ST) + (J) * 4096, offa[KH][0], offa[KH][1])
+#define KG_FRAG_O(ST, KH, X) (OUTER_W ? KG_FRAG_W(ST, KH, X) : KG_FRAG_A(ST, KH, X))
+#define KG_FRAG_I(ST, KH, X) (OUTER_W ? KG_FRAG_A(ST, KH, X) : KG_FRAG_W(ST, KH, X))
+#define KG_MFMA(O, N, WF, AF)                                                                             \
+  do {                                                                                                    \
+    const int i_ = OUTER_W ? (O) : (N), j_ = OUTER_W ? (N) : (O);                                           \
+    acc[i_][j_] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(WF, AF, acc[i_][j_], 0, 0, 0, sb[i_], 0,  \
+                                                                  sa[j_]);                                \
+  } while (0)
+#define KG_MFMA_ON(O, N, OF, IF)                                                                          \
+  do {                                                                                                    \
+    if constexpr (OUTER_W) KG_MFMA(O, N, OF, IF); else KG_MFMA(O, N, IF, OF);                              \
+  } while (0)
 
-  auto compute = [&](const u8* stage, int kt) {
-    const int sh = (kt & 3) * 8;
-    int sa[TJ], sb[TI];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) sa[j] = (int)((wa[j] >> sh) & 0xffu);
-#pragma unroll
-    for (int i = 0; i < TI; ++i) sb[i] = (int)((wb[i] >> sh) & 0xffu);
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      v8i bf[TJ], af[TI];
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-        af[i] = kg_lds_frag(stage + wtile(i) * 128, offw[kh][0], offw[kh][1]);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) bf[j] = kg_lds_frag(stage + j * 32 * 128, offa[kh][0], offa[kh][1]);
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0, 0, sb[i], 0,
-                                                                        sa[j]);
-    }
-  };
+#define KG_FP8_STEP(CUR, NXT, KTV)                                                                         \
+  do {                                                                                                    \
+    const int kt_ = (KTV);                                                                                 \
+    const int sh_ = (kt_ & 3) * 8;                                                                         \
+    int sa[TJ], sb[TI];                                                                                   \
+    _Pragma("unroll") for (int j = 0; j < TJ; ++j) sa[j] = (int)((wa[j] >> sh_) & 0xffu);                  \
+    _Pragma("unroll") for (int i = 0; i < TI; ++i) sb[i] = (int)((wb[i] >> sh_) & 0xffu);                  \
+    __builtin_amdgcn_sched_barrier(0);                                                                    \
+    /* first half: K half 0 of CUR; reads K half 1 of CUR */                                              \
+    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
+      _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                     \
+        KG_MFMA_ON(o, n, str[o & 1], res[0][n]);                                                          \
+        if (n == 0) {                                                                                     \
+          if (o + 1 < NO) str[(o + 1) & 1] = KG_FRAG_O(CUR, 0, o + 1);                                     \
+          else str[0] = KG_FRAG_O(CUR, 1, 0);                                                             \
+        }                                                                                                 \
+        if (o * NI + n < NI) res[1][o * NI + n] = KG_FRAG_I(CUR, 1, o * NI + n);                           \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+      }                                                                                                   \
+    }                                                                                                     \
+    /* second half: K half 1 of CUR; barrier; next step's scale words, its K half 0 from NXT, and the DMA \
+       of K block kt + 2 into CUR (past the last K block these read zeros / unused data, harmlessly) */   \
+    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
+      _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                     \
+        KG_MFMA_ON(o, n, str[o & 1], res[1][n]);                                                          \
+        if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_FRAG_O(CUR, 1, o + 1);                             \
+        if (o * NI + n == BAR) {                                                                          \
+          __syncthreads();                                                                                \
+          KG_LOAD_WORDS(kt_ + 1, wa, wb);                                                                 \
+        } else if (o * NI + n > BAR) {                                                                    \
+          if (n == 0 && o + 1 == NO) str[0] = KG_FRAG_O(NXT, 0, 0);                                        \
+          constexpr int NIT = NI + NQA + NQB;                                                              \
+          _Pragma("unroll") for (int u = 0; u < NIT; ++u) {                                                \
+            if (u * NSLOT / NIT != o * NI + n - BAR - 1) continue;                                         \
+            if (u < NI) res[0][u] = KG_FRAG_I(NXT, 0, u);                                                   \
+            else kg_fp8_dma<NQA, NQB, SA>(CUR, wave, ra, rw, va, vw, p.lda, woff, (kt_ + 2) * 128, u - NI); \
+          }                                                                                               \
+        }                                                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+      }                                                                                                   \
+    }                                                                                                     \
+  } while (0)
 
-  // ---- main loop: two stages, unrolled by two so each stage is its own LDS object
-  issue(st0, 0);
-  __syncthreads();   // (the barrier waits for the DMA: vmcnt(0))
+  // prologue: K block 0 in stage 0, K block 1 on its way into stage 1, block 0's first-half fragments read
+  kg_fp8_issue<NQA, NQB, SA>(st0, wave, ra, rw, va, vw, p.lda, woff, 0);
+  KG_LOAD_WORDS(0, wa, wb);
+  __syncthreads();
+  kg_fp8_issue<NQA, NQB, SA>(st1, wave, ra, rw, va, vw, p.lda, woff, 128);
+  str[0] = KG_FRAG_O(st0, 0, 0);
+#pragma unroll
+  for (int n = 0; n < NI; ++n) res[0][n] = KG_FRAG_I(st0, 0, n);
+
   int kt = 0;
   for (; kt + 2 <= KT; kt += 2) {
-    if ((kt & 3) == 0) load_words(kt);
-    issue(st1, kt + 1);
-    compute(st0, kt);
-    __syncthreads();
-    if (kt + 2 < KT) issue(st0, kt + 2);
-    compute(st1, kt + 1);
-    __syncthreads();
+    KG_FP8_STEP(st0, st1, kt);
+    KG_FP8_STEP(st1, st0, kt + 1);
   }
-  if (kt < KT) {     // odd number of K blocks: the last one is in stage 0
-    if ((kt & 3) == 0) load_words(kt);
-    compute(st0, kt);
-  }
+  if (kt < KT) KG_FP8_STEP(st0, st1, kt);     // an odd number of K blocks ends in stage 0
+  // no DMA may still be writing LDS when the workgroup retires
+  __builtin_amdgcn_s_waitcnt(0);
+#undef KG_FRAG_W
+#undef KG_LOAD_WORDS
+#undef KG_FRAG_A
+#undef KG_FRAG_O
+#undef KG_FRAG_I
+#undef KG_MFMA_ON
+#undef KG_FP8_STEP
+#undef KG_MFMA
 
   // ---- epilogue
   kg_mfma_drain();
