@@ -182,6 +182,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run three device-to-device copies of MIB MiB (calibrates HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (each GEMM shards trivially by "
@@ -191,6 +193,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {args.copy_probe} MiB device-to-device")
+        return
 
     log("generating and quantizing synthetic operands on the GPU")
     data = prepare(dev)

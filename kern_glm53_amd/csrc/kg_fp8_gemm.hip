@@ -106,39 +106,89 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   static_assert(MODE != 2 || BN == 256, "the fused epilogue quantizes 128 output columns per workgroup");
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
-  __shared__ int ps[1024];
+  __shared__ int ps[1024], tp[1024], wtot[4];
   __shared__ float xam[2][BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  const int wid = kg_xcd_remap((int)blockIdx.x, (int)gridDim.x);
 
-  int mt, nt, g = 0, m0, m_end;
+  // Tile order: groups of G = 8 row tiles, column-tile-major inside a group, so the ~32 workgroups an XCD
+  // runs at once share 8 A row tiles and ~4 weight column slices through its L2.
+  constexpr int G = 8;
+  int nt, g = 0, m0, m_end;
   if constexpr (MODE == 0) {
-    constexpr int G = 8;
+    const int wid = kg_xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int gsz = G * p.n_tiles, grp = wid / gsz, first = grp * G;
     const int gm = min(p.m_tiles - first, G), r = wid - grp * gsz;
-    mt = first + r % gm;
     nt = r / gm;
-    m0 = mt * BM;
+    m0 = (first + r % gm) * BM;
     m_end = min(p.m, m0 + BM);
   } else {
-    mt = wid / p.n_tiles;
-    nt = wid - mt * p.n_tiles;
-    for (int i = tid; i < p.groups; i += 256) ps[i] = p.psum[i];
+    // Expert g owns rows [start_g, psum[g]) with start_g = round_up128(psum[g-1]) and needs
+    // R_g = ceil(rows_g / BM) row tiles.  An exclusive prefix tp[] of R_g (a block-wide scan: each thread
+    // sums four experts, wave shuffles scan the 256 partials) numbers the live row tiles 0..total-1.
+    // Only the first total * n_tiles workgroups work; they are spread over the XCDs as in the dense case
+    // and ordered expert by expert, each expert's tiles grouped as above, so the workgroups that share
+    // an expert's weight slice run side by side on one XCD.
+    int part = 0;
+    int tl[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int e = tid * 4 + x;
+      int t = 0;
+      if (e < p.groups) {
+        const int end = p.psum[e];
+        const int start = e ? ((p.psum[e - 1] + 127) >> 7) << 7 : 0;
+        ps[e] = end;
+        t = end > start ? (end - start + BM - 1) / BM : 0;
+      }
+      tl[x] = t;
+      part += t;
+    }
+    const int lane_ = tid & 63, w_ = tid >> 6;
+    int incl = part;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane_ >= o) incl += v;
+    }
+    if (lane_ == 63) wtot[w_] = incl;
     __syncthreads();
-    m0 = mt * BM;
-    // the largest g with start(g) = round_up128(psum[g-1]) <= m0
-    int lo = 0, hi = p.groups - 1;
+    int base = incl - part;
+    for (int v = 0; v < w_; ++v) base += wtot[v];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int e = tid * 4 + x;
+      if (e < p.groups) tp[e] = base;
+      base += tl[x];
+    }
+    const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    __syncthreads();
+    const int live = total * p.n_tiles;
+    if ((int)blockIdx.x >= live) return;       // past the live tiles (uniform exit)
+    const int wid = kg_xcd_remap((int)blockIdx.x, live);
+    const int rt_flat = wid / p.n_tiles;
+    int lo = 0, hi = p.groups - 1;             // the last g with tp[g] <= rt_flat (it has R_g > 0)
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      const int start = ((ps[mid - 1] + 127) >> 7) << 7;
-      if (start <= m0) lo = mid; else hi = mid - 1;
+      if (tp[mid] <= rt_flat) lo = mid; else hi = mid - 1;
     }
     g = lo;
-    m_end = min(ps[g], m0 + BM);
-    if (m0 >= m_end) return;                 // padding block: no expert owns it (uniform exit)
+    const int rg = (g + 1 < p.groups ? tp[g + 1] : total) - tp[g];
+    const int l = wid - tp[g] * p.n_tiles, grp = l / (G * p.n_tiles);
+    const int gm = min(rg - grp * G, G), r = l - grp * G * p.n_tiles;
+    nt = r / gm;
+    const int start = g ? ((ps[g - 1] + 127) >> 7) << 7 : 0;
+    m0 = start + (grp * G + r % gm) * BM;
+    m_end = min(min(ps[g], p.rows), m0 + BM);   // rows past the buffer are never touched
+    // values read from LDS are per-lane to the compiler; declaring them uniform keeps the buffer
+    // resources built from them in SGPRs (otherwise every buffer load becomes a waterfall loop)
+    g = __builtin_amdgcn_readfirstlane(g);
+    nt = __builtin_amdgcn_readfirstlane(nt);
+    m0 = __builtin_amdgcn_readfirstlane(m0);
+    m_end = __builtin_amdgcn_readfirstlane(m_end);
+    if (m0 >= m_end) return;
   }
   const int n0 = nt * (MODE == 2 ? BN / 2 : BN);
   const int kw = (p.k + 511) >> 9, KT = p.k >> 7;
@@ -325,8 +375,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   } else {
     // silu(g) * u in registers: gate tile i pairs with up tile i + TI/2 at the same output columns.
     // Same arithmetic as the unfused pair (bf16 gate_up, then glm_silu_mul_quant), so results match it
-    // bit for bit.
-    float vals[TI / 2][TJ][16];
+    // bit for bit.  The product overwrites the gate accumulator, which keeps it out of the VGPR budget.
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       float am = 0.0f;
@@ -337,7 +386,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
           // the gate_up output is bf16 in the reference (g13), so g and u are rounded before the SiLU
           const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
                                            kg_bf16_to_f32(kg_f32_to_bf16(acc[i + TI / 2][j][r])));
-          vals[i][j][r] = v;
+          acc[i][j][r] = v;
           am = fmaxf(am, fabsf(v));
         }
       am = fmaxf(am, __shfl_xor(am, 32, 64));
@@ -357,7 +406,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int cn = n0 + wn * (BN / 4) + i * 32 + rr * 8 + (lane >> 5) * 4;
-          const float* v = &vals[i][j][rr * 4];
+          const v16f& a4 = acc[i][j];
+          const float v[4] = {a4[rr * 4], a4[rr * 4 + 1], a4[rr * 4 + 2], a4[rr * 4 + 3]};
           *reinterpret_cast<u32*>(qrow + cn) = kg_e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
         }
       if (wn == 0 && lane < 32)
@@ -370,8 +420,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 
 template __global__ void kg_fp8_gemm_kernel<256, 256, 0>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_kernel<128, 128, 0>(const KgFp8Args);
-template __global__ void kg_fp8_gemm_kernel<128, 256, 1>(const KgFp8Args);
-template __global__ void kg_fp8_gemm_kernel<128, 256, 2>(const KgFp8Args);
+template __global__ void kg_fp8_gemm_kernel<256, 256, 1>(const KgFp8Args);
+template __global__ void kg_fp8_gemm_kernel<256, 256, 2>(const KgFp8Args);
 
 template <int BM, int BN, int MODE>
 static int kg_fp8_launch(KgFp8Args& p, int total, hipStream_t st) {
@@ -412,10 +462,10 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
   p.psum = psum, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows;
   p.groups = groups;
-  p.m_tiles = rows / 128, p.n_tiles = (n + 255) / 256;
+  p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n + 255) / 256;   // an upper bound of the live tiles
   const long long total = (long long)p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
-  return kg_fp8_launch<128, 256, 1>(p, (int)total, (hipStream_t)stream);
+  return kg_fp8_launch<256, 256, 1>(p, (int)total, (hipStream_t)stream);
 }
 
 extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, const void* sfb,
@@ -430,8 +480,8 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb;
   p.psum = psum, p.q = (u8*)q, p.qsf = (u8*)sf, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda;
   p.ldc = n, p.sfa_rows = sfa_rows, p.groups = groups, p.sf_rows = sf_rows;
-  p.m_tiles = rows / 128, p.n_tiles = (n / 2) / 128;
+  p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n / 2) / 128;
   const long long total = (long long)p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
-  return kg_fp8_launch<128, 256, 2>(p, (int)total, (hipStream_t)stream);
+  return kg_fp8_launch<256, 256, 2>(p, (int)total, (hipStream_t)stream);
 }
