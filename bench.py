@@ -36,6 +36,24 @@ DENSE = [  # name, n, k, ldc  (scripts/gen.py:183-186: a.shared, b.shared, o)
 ]
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "fp8_gemm_bench_m16384_hbm_traffic.txt")
+
+
+def measured_traffic(launch: str):
+    """HBM bytes per launch of `launch` as recorded by the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by the
+    copy-kernel calibration) in the committed profile summary; None when it has no entry."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == launch:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -107,11 +125,16 @@ def prepare(dev):
     moe["shared"] = torch.zeros(M, H, dtype=torch.bfloat16, device=dev)
     moe["out"] = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
     moe["mcap"] = mcap
+    moe["g13"] = (torch.randn(mcap, 2 * INTER, generator=synth.generator(8, "cuda"), device=dev) * 2).to(torch.bfloat16)
     data["moe"] = moe
+    data["x_h"] = synth.activations(M, H, synth.generator(99, "cuda"), device=dev)
+    data["xq_h"] = torch.empty(M, H, dtype=torch.uint8, device=dev)
+    data["xsf_h"] = torch.empty(sfw(H) * M * 4, dtype=torch.uint8, device=dev)
     torch.cuda.synchronize()
     counts = moe["counts"][:EXPERTS].cpu()
     moe["R"] = int(counts.sum())
     moe["blocks"] = int(((counts + 127) // 128).sum())
+    moe["tpad_rows"] = 128 * moe["blocks"]
     moe["max_count"], moe["min_count"] = int(counts.max()), int(counts.min())
     return data
 
@@ -138,17 +161,90 @@ def launches(data):
 
 
 def glue_launches(data):
+    """The glue around the MoE GEMMs: (name, launch, algorithmic HBM bytes or None when latency-bound)."""
     from kern_glm53_amd import ops
 
     m = data["moe"]
     xq, xsf = data["q_a_kv_a"]["a"], data["q_a_kv_a"]["sfa"]
+    K, I = H, INTER
+    tp = m["tpad_rows"]
     return [
+        ("quant", lambda: ops.quant(data["x_h"], K, data["xq_h"], data["xsf_h"], M, K, M),
+         M * K * 3 + M * K // 128),
         ("routing", lambda: ops.routing(m["ids"], m["counts"], m["cta_batch"], m["cta_limit"], m["nne"], m["tpad"],
-                                        m["route_map"], m["exp2perm"], T=M)),
-        ("moe_psum", lambda: ops.moe_psum(m["counts"], m["psum"])),
-        ("moe_gather", lambda: ops.moe_gather(xq, xsf, M, m["exp2perm"], m["mq"], m["msf"], m["mcap"], T=M)),
-        ("moe_combine", lambda: ops.moe_combine(m["f2"], m["exp2perm"], m["wts"], m["shared"], m["out"], M)),
+                                        m["route_map"], m["exp2perm"], T=M), None),
+        ("moe_psum", lambda: ops.moe_psum(m["counts"], m["psum"]), None),
+        ("moe_gather", lambda: ops.moe_gather(xq, xsf, M, m["exp2perm"], m["mq"], m["msf"], m["mcap"], T=M),
+         (m["R"] + M) * (K + K // 128)),
+        ("silu_mul_quant", lambda: ops.silu_mul_quant(m["g13"], I, m["mq2"], m["msf2"], m["mcap"], m["tpad"],
+                                                      m["mcap"]), tp * (4 * I + I + I // 128)),
+        ("moe_combine", lambda: ops.moe_combine(m["f2"], m["exp2perm"], m["wts"], m["shared"], m["out"], M),
+         M * (TOPK * 2 * K + 2 * 2 * K + TOPK * 8)),
     ]
+
+
+def aux_prepare(data, dev):
+    """Operands of the absorbed-MLA batched GEMMs and the indexer's MQA logits at the M = 16384 chunk of one
+    65536-token sequence (scripts/gen.py:136-139, 178-179, 376, 382-387, 401)."""
+    from kern_glm53_amd import synth
+
+    g = synth.generator(900, "cuda")
+    bf = lambda *s: (torch.randn(*s, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    aux = {}
+    # W_UK: A = q_b's output viewed [r][h][0:192] (row 40960 B, head 512 B), B = wuk [64][512][192],
+    # D = qmla [r][64][576] columns 0:512 (row 73728 B, head 1152 B)
+    aux["qb"] = data["q_b"]["c"]
+    aux["wuk"] = bf(64, 512, 192)
+    aux["qmla"] = torch.zeros(M, 64, 576, dtype=torch.bfloat16, device=dev)
+    # W_UV: A = o [r][64][512], B = kvb rows h*448 + 192 + d (row 1024 B, head 458752 B), D = ov [r][64][256]
+    aux["o"] = bf(M, 64, 512)
+    aux["kvb"] = bf(64 * 448, 512)
+    aux["ov"] = torch.empty(M, 64, 256, dtype=torch.bfloat16, device=dev)
+    # MQA logits: the last 16384 rows of a 65536-token sequence, causal: ks = 0, ke = p + 1
+    ctx = 65536
+    codes = lambda *s: (torch.randint(0, 0x78, s, generator=g, device=dev, dtype=torch.int32)
+                        | (torch.randint(0, 2, s, generator=g, device=dev, dtype=torch.int32) << 7)).to(torch.uint8)
+    aux["iq"] = codes(M, 32, 128)
+    aux["kg"] = codes(ctx, 128)
+    aux["ksf"] = torch.exp2(torch.randint(-8, 0, (ctx,), generator=g, device=dev).float())
+    aux["w"] = torch.randn(M, 32, generator=g, device=dev) * (128 ** -0.5) * (32 ** -0.5)
+    aux["ks"] = torch.zeros(M, dtype=torch.int32, device=dev)
+    aux["ke"] = (torch.arange(M, dtype=torch.int32, device=dev) + (ctx - M) + 1)
+    aux["logits"] = torch.empty(M, ctx, dtype=torch.float32, device=dev)
+    aux["ctx"] = ctx
+    aux["klen"] = sum(range(ctx - M + 1, ctx + 1))
+    return aux
+
+
+def aux_launches(aux):
+    """(name, launch, algorithmic flops, algorithmic HBM bytes, bound) for the non-headline GEMM rows."""
+    from kern_glm53_amd import ops
+
+    ctx, klen = aux["ctx"], aux["klen"]
+    return [
+        ("w_uk_bf16_batched", lambda: ops.bf16_batched(aux["qb"], aux["wuk"], aux["qmla"], M, n=512, k=192, rows=M,
+                                                        a_strides=(40960, 512), b_strides=(384, 196608),
+                                                        d_strides=(73728, 1152)),
+         2.0 * M * 64 * 512 * 192, M * 64 * (192 + 512) * 2 + 64 * 512 * 192 * 2, "hbm"),
+        ("w_uv_bf16_batched", lambda: ops.bf16_batched(aux["o"], aux["kvb"][192:], aux["ov"], M, n=256, k=512, rows=M,
+                                                        a_strides=(65536, 1024), b_strides=(1024, 458752),
+                                                        d_strides=(32768, 512)),
+         2.0 * M * 64 * 256 * 512, M * 64 * (512 + 256) * 2 + 64 * 256 * 512 * 2, "hbm"),
+        ("mqa_logits", lambda: ops.mqa_logits(aux["iq"], aux["kg"], aux["ksf"], aux["w"], aux["ks"], aux["ke"],
+                                              aux["logits"], M, ctx, ctx),
+         2.0 * 128 * 32 * klen, 4 * klen + M * 32 * 128 + ctx * 132 + M * 136, "mfma"),
+    ]
+
+
+def time_launch(fn, stream, iters=5):
+    fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
 
 
 def cpu_baseline(data, rows=2048, runs=3):
@@ -237,21 +333,28 @@ def main():
     dflops = dict((n, f) for n, f, _ in L)[dom]
     roofline = {"bound": "mfma", "achieved": round(dflops / (per[dom]["ms"] * 1e-3) / 1e12, 2),
                 "peak": PEAK_FP8 / 1e12, "unit": "TFLOP/s",
-                "frac": round(dflops / (per[dom]["ms"] * 1e-3) / PEAK_FP8, 4), "traffic": None, "kernel": dom}
+                "frac": round(dflops / (per[dom]["ms"] * 1e-3) / PEAK_FP8, 4), "traffic": measured_traffic(dom),
+                "kernel": dom}
     log("per kernel: " + ", ".join(f"{k} {v['ms']:.3f} ms {v['tflops']:.0f} TF/s" for k, v in per.items()))
 
-    # glue around the MoE GEMMs (not part of `value`): mean over a few timed launches
+    # glue around the MoE GEMMs and the other GEMM rows of the path (not part of `value`)
     glue = {}
-    for name, fn in glue_launches(data):
-        fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(5):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        glue[name] = round(e0.elapsed_time(e1) / 5 * 1e3, 1)
-    log("glue (us): " + ", ".join(f"{k} {v}" for k, v in glue.items()))
+    for name, fn, nbytes in glue_launches(data):
+        ms = time_launch(fn, stream)
+        glue[name] = {"us": round(ms * 1e3, 1)}
+        if nbytes:
+            glue[name].update(gbps=round(nbytes / (ms * 1e-3) / 1e9, 1), frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM, 4))
+    log("glue (us): " + ", ".join(f"{k} {v['us']}" for k, v in glue.items()))
+    aux = {}
+    aux_data = aux_prepare(data, dev)
+    for name, fn, flops, nbytes, bound in aux_launches(aux_data):
+        ms = time_launch(fn, stream)
+        aux[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                     "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": bound,
+                     "frac": round(flops / (ms * 1e-3) / PEAK_FP8 if bound == "mfma" else
+                                   nbytes / (ms * 1e-3) / PEAK_HBM, 4)}
+    del aux_data
+    log("aux: " + ", ".join(f"{k} {v['ms']:.3f} ms ({v['tflops']:.0f} TF/s, {v['gbps']:.0f} GB/s)" for k, v in aux.items()))
 
     cpu = None
     if not args.no_cpu:
@@ -270,7 +373,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": per,
-        "glue_us": glue,
+        "glue": glue,
+        "aux": aux,
     }
     print(json.dumps(line), flush=True)
 

@@ -22,7 +22,7 @@ extern "C" {
 /* ---------------------------------------------------------------- GEMMs (module glm_deepgemm) */
 
 /* fp8 1d1d dense GEMM.  Replaces the `fp8_gemm(n, k, rows, lda, ldc, sfa_rows)` op with groups = 1
- * (scripts/glm_ops.py:194-215; kernel instance source/glm_deepgemm.cu:38-39):
+ * (scripts/glm_ops.py:57-78; kernel instance source/glm_deepgemm.cu:38-39):
  *   C[r][0:n] = bf16( sum_kb 2^(sfa[r,kb]-127) 2^(sfb[c,kb]-127) sum_{k in kb} A[r][k] W[c][k] ), r < m,
  * f32 accumulation.  a: e4m3 [rows][lda]; w: e4m3 [n][k]; sfa: words [k/512][sfa_rows]; sfb: words
  * [k/512][n] (one word per weight row); c: bf16 [rows][ldc], columns [n, ldc) untouched.
@@ -31,7 +31,7 @@ int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, 
                 int rows, int lda, int ldc, int sfa_rows, void* stream);
 
 /* fp8 m-grouped GEMM in the psum layout.  Replaces `fp8_gemm(..., groups)` with groups > 1
- * (scripts/glm_ops.py:194-215, 58-61 of the docstring; instance source/glm_deepgemm.cu:40-41):
+ * (scripts/glm_ops.py:57-78, docstring 58-61; instance source/glm_deepgemm.cu:40-41):
  * for every group g, rows [round_up128(psum[g-1]), psum[g]) of C (psum[-1] = 0) are the dense GEMM of
  * the same rows of A with weight rows [g n, (g+1) n) and scale words [g k/512, (g+1) k/512).  Rows no group
  * owns are left untouched.  psum: device int32 [groups] (glm_moe_psum's output). */
@@ -47,17 +47,18 @@ int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, c
                                 int groups, int n, int k, int rows, int lda, int sfa_rows, void* q, void* sf,
                                 int sf_rows, void* stream);
 
-/* bf16 GEMM batched over heads.  Replaces `bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:225-236;
+/* bf16 GEMM batched over heads.  Replaces `bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:88-99;
  * instance source/glm_deepgemm.cu:42-43):  D[r][h][0:n] = bf16(sum_k A[r][h][k] B[h][d][k]), f32
  * accumulation, r < m, h < heads.  Every operand is a byte-strided view: element (r, h, x) of A at
  * a + r*a_rs + h*a_hs + 2x, of B (h, d, x) at b + d*b_rs + h*b_hs + 2x, of D (r, h, d) at d + r*d_rs +
- * h*d_hs + 2d.  Requires k % 32 == 0, n % 32 == 0, strides multiples of 16 bytes. */
+ * h*d_hs + 2d.  Requires k % 64 == 0, n % 4 == 0, A / B strides multiples of 16 bytes and D strides of 8
+ * (the reference's W_UK has k = 192, W_UV k = 512). */
 int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
                     long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs, long long d_hs,
                     void* stream);
 
 /* The indexer's fp8 MQA logits (compressed rows).  Replaces the `sm100_mqa_logits` launch of the
- * `indexer(j, r, kv_cap)` op (scripts/glm_ops.py:246-268; instance source/glm_deepgemm.cu:44-45): for
+ * `indexer(j, r, kv_cap)` op (scripts/glm_ops.py:109-135; instance source/glm_deepgemm.cu:44-45): for
  * r < num_q and j < ke[r] - ks[r],
  *   logits[r * stride + j] = sum_{h<32} w[r][h] * relu(ksf[ks[r]+j] * sum_{d<128} q[r][h][d] kv[ks[r]+j][d]).
  * q: e4m3 [num_q][32][128]; kv: e4m3 [num_kv][128]; ksf f32 [num_kv] (powers of two > 0); w f32 [num_q][32];
@@ -76,7 +77,7 @@ int kg_quant(const void* x, int ldx, void* q, void* sf, int sf_rows, int K, int 
  * live rows.  The exp is this library's (kg_exp), not CUDA's __expf. */
 int kg_silu_mul_quant(const void* gu, int I, void* q, void* sf, int sf_rows, const int* n, int rows, void* stream);
 
-/* FlashInfer routingPrecomputed tables (the `routing(experts, topk, tile)` op, scripts/glm_ops.py:344-370;
+/* FlashInfer routingPrecomputed tables (the `routing(experts, topk, tile)` op, scripts/glm_ops.py:207-233;
  * three launches as there).  ids int32 [T][topk] -> counts [2*experts] (upper half zero), cta_batch /
  * cta_limit [ctas], num_non_exiting [1], total_padded [1], route_map [mcap], exp2perm [T][topk];
  * expert e's rows start at 2^tile_log2 times its CTA offset and, within an expert, follow ascending

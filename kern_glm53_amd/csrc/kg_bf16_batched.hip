@@ -1,6 +1,6 @@
 // bf16 GEMM batched over heads (MLA's W_UK absorption and W_UV up-projection) on gfx950:
 // D[r][h][0:n] = bf16(sum_k A[r][h][k] B[h][d][k]), f32 accumulation, every operand a byte-strided view
-// (source/glm_deepgemm.cu:26-33, 42-43; scripts/glm_ops.py:225-236; shapes scripts/gen.py:136-139).
+// (source/glm_deepgemm.cu:26-33, 42-43; scripts/glm_ops.py:88-99; shapes scripts/gen.py:136-139).
 //
 // HBM-bound (102-169 flop/B against a bf16 ridge of ~315): the design goal is streaming A and D once at
 // full width while the MFMA work hides under it.

@@ -1,6 +1,6 @@
 // fp8 1d1d GEMMs of kern-glm53's `glm_deepgemm` path on gfx950: e4m3 x e4m3 with UE8M0 128-K-block
 // scales on both operands, f32 accumulation, bf16 out (source/glm_deepgemm.cu:17-24, 38-41;
-// scripts/glm_ops.py:194-215).  One kernel template, three modes:
+// scripts/glm_ops.py:57-78).  One kernel template, three modes:
 //   MODE 0  dense:    C[0:m, 0:n] = A . W^T
 //   MODE 1  psum:     per expert g, rows [round_up128(psum[g-1]), psum[g]) with W rows [g n, (g+1) n)
 //   MODE 2  psum + SiLU-mul + per-128 e4m3 requant epilogue (gate columns [0, n/2), up [n/2, n))

@@ -96,7 +96,7 @@ extern "C" int kg_silu_mul_quant(const void* gu, int I, void* q, void* sf, int s
 
 // ============================================================================ routing plan (a6)
 
-// Three launches, as the reference's routing op (scripts/glm_ops.py:365-370):
+// Three launches, as the reference's routing op (scripts/glm_ops.py:230-233):
 //   1. kg_route_count: each workgroup histograms one segment of KG_SEG expanded rows into the scratch
 //      table seg[s][e];
 //   2. kg_route_plan (one workgroup, a thread per expert): totals, the CTA offsets by a block-wide scan,

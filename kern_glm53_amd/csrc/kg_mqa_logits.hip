@@ -1,5 +1,5 @@
 // The lightning indexer's fp8 MQA logits on gfx950 (source/glm_deepgemm.cu:35, 44-45;
-// scripts/glm_ops.py:239-268): for query row r and key j in [ks[r], ke[r]),
+// scripts/glm_ops.py:101-135): for query row r and key j in [ks[r], ke[r]),
 //   logits[r * stride + (j - ks[r])] = sum_{h<32} w[r][h] * relu(ksf[j] * sum_{d<128} q[r][h][d] kv[j][d]).
 // The key scale is a UE8M0 power of two (> 0), so it leaves the head sum exactly: the kernel forms
 // ksf[j] * sum_h w[r][h] relu(q_h . k_j), which equals the reference expression in exact arithmetic and

@@ -28,7 +28,7 @@ def sf_words(k: int) -> int:
 
 
 def counts_len(experts: int = EXPERTS) -> int:
-    """Length of the routing `counts` buffer (scripts/glm_ops.py:340-341)."""
+    """Length of the routing `counts` buffer (scripts/glm_ops.py:203-204)."""
     return max(512, 2 * experts)
 
 
@@ -47,7 +47,7 @@ def _stream():
 # ------------------------------------------------------------------ GEMMs
 
 def fp8_gemm(a, w, sfa, sfb, c, m: int, *, n: int, k: int, rows: int, lda: int, ldc: int, sfa_rows: int):
-    """`fp8_gemm(n, k, rows, lda, ldc, sfa_rows)` with groups = 1 (scripts/glm_ops.py:194-215):
+    """`fp8_gemm(n, k, rows, lda, ldc, sfa_rows)` with groups = 1 (scripts/glm_ops.py:57-78):
     C[0:m, 0:n] = A . W^T with UE8M0 128-block scales on both operands, bf16 out."""
     call("kg_fp8_gemm", _ptr(a), _ptr(w), _ptr(sfa), _ptr(sfb), _ptr(c), m, n, k, rows, lda, ldc, sfa_rows,
          _stream())
@@ -55,7 +55,7 @@ def fp8_gemm(a, w, sfa, sfb, c, m: int, *, n: int, k: int, rows: int, lda: int, 
 
 def fp8_gemm_psum(a, w, sfa, sfb, c, psum, *, n: int, k: int, rows: int, lda: int, ldc: int, sfa_rows: int,
                   groups: int = EXPERTS):
-    """`fp8_gemm(..., groups)` in the psum layout (scripts/glm_ops.py:194-215): expert g's rows end at
+    """`fp8_gemm(..., groups)` in the psum layout (scripts/glm_ops.py:57-78): expert g's rows end at
     psum[g] and start at the previous end rounded up to 128."""
     call("kg_fp8_gemm_psum", _ptr(a), _ptr(w), _ptr(sfa), _ptr(sfb), _ptr(c), _ptr(psum), groups, n, k, rows, lda,
          ldc, sfa_rows, _stream())
@@ -70,14 +70,14 @@ def fp8_gemm_psum_silu_quant(a, w, sfa, sfb, psum, q, sf, *, n: int, k: int, row
 
 
 def bf16_batched(a, b, d, m: int, *, n: int, k: int, rows: int, a_strides, b_strides, d_strides, heads: int = 64):
-    """`bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:225-236): D[r][h][:n] = A[r][h][:k] . B[h][:n][:k]^T
+    """`bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:88-99): D[r][h][:n] = A[r][h][:k] . B[h][:n][:k]^T
     with each operand's byte strides (row, head) as in the reference."""
     call("kg_bf16_batched", _ptr(a), _ptr(b), _ptr(d), m, n, k, rows, heads, int(a_strides[0]), int(a_strides[1]),
          int(b_strides[0]), int(b_strides[1]), int(d_strides[0]), int(d_strides[1]), _stream())
 
 
 def mqa_logits(iq, kg, ksf, w, ks, ke, logits, num_q: int, num_kv: int, stride: int):
-    """The MQA-logits launch of the `indexer` op (scripts/glm_ops.py:246-268): compressed logits rows."""
+    """The MQA-logits launch of the `indexer` op (scripts/glm_ops.py:109-135): compressed logits rows."""
     call("kg_mqa_logits", _ptr(iq), _ptr(kg), _ptr(ksf), _ptr(w), _ptr(ks), _ptr(ke), _ptr(logits), num_q, num_kv,
          stride, _stream())
 
@@ -96,7 +96,7 @@ def silu_mul_quant(gu, I: int, q, sf, sf_rows: int, n, rows: int):
 
 def routing(ids, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, *, T: int,
             experts: int = EXPERTS, topk: int = TOPK, tile: int = TILE):
-    """`routing(experts, topk, tile)` (scripts/glm_ops.py:344-370): FlashInfer routingPrecomputed tables."""
+    """`routing(experts, topk, tile)` (scripts/glm_ops.py:207-233): FlashInfer routingPrecomputed tables."""
     assert tile & (tile - 1) == 0, "tile must be a power of two"
     call("kg_moe_routing", _ptr(ids), T, topk, experts, tile.bit_length() - 1, _ptr(counts), _ptr(cta_batch),
          _ptr(cta_limit), _ptr(num_non_exiting), _ptr(total_padded), _ptr(route_map), _ptr(exp2perm), _stream())

@@ -147,7 +147,7 @@ void kgo_head_quant(const float* x, int rows, int heads, u8* q, float* sc) {
 
 /* ---------------------------------------------------------------- MoE routing plan (a6, a7) */
 
-/* FlashInfer routingPrecomputed tables over precomputed top-k ids (scripts/glm_ops.py:344-370, the
+/* FlashInfer routingPrecomputed tables over precomputed top-k ids (scripts/glm_ops.py:207-233, the
  * docstring at 345-347; buffers scripts/gen.py:285-293; the CTA offset convention of
  * source/glm_glue.cu:446-447).  Within an expert the expanded rows are ranked by ascending expanded
  * index t * topk + k.  counts has 2 * experts entries: [0, experts) the per-expert row counts, the

@@ -140,7 +140,7 @@ def head_quant(x: np.ndarray):
 # ------------------------------------------------------------------ MoE routing plan (a6-a8, a10, a11)
 
 def moe_routing(ids: np.ndarray, experts: int = 256, tile_log2: int = 7):
-    """FlashInfer routingPrecomputed tables (scripts/glm_ops.py:344-370) in canonical order."""
+    """FlashInfer routingPrecomputed tables (scripts/glm_ops.py:207-233) in canonical order."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     T, topk = ids.shape
     mcap = topk * T + experts * (1 << tile_log2)
@@ -244,7 +244,7 @@ def scale_exponents(sf_bytes, rows_total: int, k: int, row0: int = 0, nrows: int
                     word_row0: int = 0) -> torch.Tensor:
     """The per-(row, 128-K-block) UE8M0 exponent bytes of a packed scale buffer: byte (kb & 3) of word
     (word_row0 + (kb >> 2)) * rows_total + row (scripts/gen.py:72, source/glm_glue.cu:81-83,
-    scripts/glm_ops.py:206-209).  Returns uint8 [nrows][k / 128]."""
+    scripts/glm_ops.py:71-72).  Returns uint8 [nrows][k / 128]."""
     sf = torch.as_tensor(np.ascontiguousarray(sf_bytes)).view(torch.uint8).reshape(-1)
     nrows = rows_total - row0 if nrows is None else nrows
     nkb = k // 128
@@ -262,7 +262,7 @@ def dequant(q: torch.Tensor, exps: torch.Tensor) -> torch.Tensor:
 
 
 def fp8_gemm(a, w, sfa, sfb, m, n, k, lda, sfa_rows, dtype=torch.float32) -> torch.Tensor:
-    """DeepGEMM fp8 1d1d Normal (source/glm_deepgemm.cu:38-39; scripts/glm_ops.py:194-215):
+    """DeepGEMM fp8 1d1d Normal (source/glm_deepgemm.cu:38-39; scripts/glm_ops.py:57-78):
     C[0:m, 0:n] = A[0:m, 0:k] . W[0:n, 0:k]^T with both operands' UE8M0 128-block scales, as an
     fp32 dequantize-then-matmul (exact products, power-of-two scales).  Returns f32 [m][n]."""
     A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)[:m, :k]
@@ -301,7 +301,7 @@ def fp8_window_bound(a, w, sfa, sfb, m, n, k, lda, sfa_rows, row0=0, w_row0=0, s
 
 
 def psum_ranges(psum: np.ndarray):
-    """Expert g's live rows [round_up128(psum[g-1]), psum[g]) with psum[-1] = 0 (scripts/glm_ops.py:195-198)."""
+    """Expert g's live rows [round_up128(psum[g-1]), psum[g]) with psum[-1] = 0 (scripts/glm_ops.py:59-61)."""
     out, prev = [], 0
     for g, end in enumerate(np.asarray(psum).tolist()):
         start = (prev + 127) // 128 * 128
@@ -322,7 +322,7 @@ def fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows
 
 
 def fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows, abs_too=False):
-    """DeepGEMM fp8 m-grouped psum layout (source/glm_deepgemm.cu:40-41; scripts/glm_ops.py:194-215):
+    """DeepGEMM fp8 m-grouped psum layout (source/glm_deepgemm.cu:40-41; scripts/glm_ops.py:57-78):
     for every expert g, its rows of C from its rows of A and its weight rows [g n, (g+1) n) with scale
     words [g k/512, (g+1) k/512).  Returns (f32 C [rows][n] with NaN on rows no expert owns, abs-sum)."""
     A = torch.as_tensor(np.ascontiguousarray(a)).view(torch.uint8).reshape(-1, lda)
@@ -344,7 +344,7 @@ def fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, lda, sfa_rows, abs_t
 
 
 def bf16_batched(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
-    """DeepGEMM bf16 Batched (source/glm_deepgemm.cu:42-43; scripts/glm_ops.py:225-236): D[r][h][d] =
+    """DeepGEMM bf16 Batched (source/glm_deepgemm.cu:42-43; scripts/glm_ops.py:88-99): D[r][h][d] =
     sum_k A[r][h][k] B[h][d][k] with f32 accumulation.  A [rows][heads][k], B [heads][n][k], both bf16
     tensors (any strides); returns f32 [rows][heads][n]."""
     a = A.to(torch.float32).permute(1, 0, 2).contiguous()   # [h][r][k]
@@ -353,7 +353,7 @@ def bf16_batched(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
 
 
 def mqa_logits(q8, k8, ksf, w, ks, ke, num_q, stride):
-    """DeepGEMM fp8 MQA logits (source/glm_deepgemm.cu:44-45; scripts/glm_ops.py:239-268): for row r < num_q
+    """DeepGEMM fp8 MQA logits (source/glm_deepgemm.cu:44-45; scripts/glm_ops.py:101-135): for row r < num_q
     and j < ke[r] - ks[r], logits[r][j] = sum_h w[r][h] * relu(ksf[ks[r]+j] * (q[r][h] . k[ks[r]+j])),
     evaluated in f64 from exact e4m3 values.  Entries at or past ke - ks are NaN (unspecified)."""
     qd = decode_e4m3_t(torch.as_tensor(np.ascontiguousarray(q8)).view(torch.uint8)).to(torch.float64)

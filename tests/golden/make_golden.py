@@ -1,6 +1,6 @@
 """Writes the golden fixtures of this directory: seeded inputs and the oracle's outputs for each op of the path,
 small enough to commit.  The reference ships no vectors for this path (its only known-answer test is
-fast_div(16) in scripts/glm_ops.py:337), so these fixtures are the pin that travels with the repository:
+fast_div(16) in scripts/glm_ops.py:200), so these fixtures are the pin that travels with the repository:
 the CPU suite checks that the oracle still reproduces them, the GPU suite that the HIP kernels do.
 
     python tests/golden/make_golden.py

@@ -1,7 +1,7 @@
 """Pins the oracle itself (CPU only).  Each check is independent of the restatement it checks: torch's
 float8 cast, closed forms from math.frexp, numpy cumsum / bincount, exact rational arithmetic, brute-force
 loops, and single-nonzero probes that fix every index of the scale layouts.  The reference ships no
-golden vectors for this path; its only known-answer test (fast_div(16), scripts/glm_ops.py:337) belongs
+golden vectors for this path; its only known-answer test (fast_div(16), scripts/glm_ops.py:200) belongs
 to the routing kernel's parameter pack, which this build's routing entry point does not use."""
 import math
 from fractions import Fraction
@@ -235,7 +235,7 @@ def test_psum_closed_form():
         b = (c + 127) // 128
         want = 128 * (np.cumsum(b) - b) + c
         assert np.array_equal(ref.moe_psum(c.astype(np.int32)), want.astype(np.int32))
-        # each expert's live range starts at the previous end rounded up to 128 (scripts/glm_ops.py:196-197)
+        # each expert's live range starts at the previous end rounded up to 128 (scripts/glm_ops.py:60-61)
         for g, (s0, s1) in enumerate(ref.psum_ranges(want)):
             assert s0 == 128 * (np.cumsum(b) - b)[g] and s1 - s0 == c[g]
 
@@ -328,6 +328,10 @@ def test_router_topk_brute_force():
                          + np.float32(np.float32(s[1] + s[5]) + np.float32(s[3] + s[7])))
         want = (s / np.float32(den + np.float32(1e-20))).astype(np.float32) * np.float32(2.5)
         assert np.array_equal(wts[b], want.astype(np.float32))
+        # independent of the summation tree: within a few f32 ulps of the float64 normalisation
+        s64 = 1.0 / (1.0 + np.exp(-S[b][order].astype(np.float64)))
+        w64 = s64 / s64.sum() * 2.5
+        assert np.all(np.abs(wts[b] - w64) <= 6 * np.spacing(np.float32(w64)))
     assert idx[0, 0] == 10 and idx[0, 1] == 20
 
 
