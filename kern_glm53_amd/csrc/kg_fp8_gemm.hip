@@ -71,30 +71,109 @@ KG_DEV int kg_wrow(int n0, int half, int r) {
 }
 
 // One K block of both operand tiles, HBM -> LDS: per wave NQA (A) and NQB (W) buffer_load ... lds of 1 KB
-// (8 rows x 128 bytes); the lane offsets va / vw carry the row-in-8 and the swizzled chunk.
+// (8 rows x 128 bytes).  LDS row r keeps 16-byte chunk c of the K block in slot c ^ ((r >> 1) & 7): the 16
+// rows one ds_read_b128 phase touches then cover all 64 banks once.  A DMA instruction covers 8 rows
+// starting at a multiple of 8, so its lanes' swizzle depends on the instruction's parity only: the lane
+// offsets va / vw (row-in-8 and swizzled chunk) come in an even and an odd version.
 template <int NQA, int NQB, int SA>
-KG_DEV void kg_fp8_issue(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw, unsigned va,
-                         unsigned vw, int lda, const int* woff, int ko) {
+KG_DEV void kg_fp8_issue(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
+                         const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko) {
+  // a buffer load's range check covers its VGPR offset only: the row offsets go there, K into the scalar
 #pragma unroll
   for (int q = 0; q < NQA; ++q)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16, va,
-                                             (wave * NQA + q) * 8 * lda + ko, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16,
+                                             va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda), ko, 0, 0);
 #pragma unroll
   for (int q = 0; q < NQB; ++q)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q) * 1024), 16, vw,
-                                             woff[q] + ko, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q) * 1024), 16,
+                                             vw[q & 1] + (unsigned)woff[q], ko, 0, 0);
 }
 
 // DMA instruction q of one K block for this wave: q < NQA an A chunk, else a W chunk.
 template <int NQA, int NQB, int SA>
-KG_DEV void kg_fp8_dma(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw, unsigned va,
-                       unsigned vw, int lda, const int* woff, int ko, int q) {
+KG_DEV void kg_fp8_dma(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
+                       const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko, int q) {
   if (q < NQA)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16, va,
-                                             (wave * NQA + q) * 8 * lda + ko, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16,
+                                             va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda), ko, 0, 0);
   else
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q - NQA) * 1024), 16,
-                                             vw, woff[q - NQA] + ko, 0, 0);
+                                             vw[(q - NQA) & 1] + (unsigned)woff[q - NQA], ko, 0, 0);
+}
+
+// Epilogue of one BM x BN output tile held in acc (after the K loop and kg_mfma_drain): bf16 stores of the
+// rows [m0, m_end) (modes 0, 1), or the fused SiLU-mul + e4m3 requant of the gate / up column pairs (mode 2).
+template <int BM, int BN, int MODE>
+KG_DEV void kg_fp8_epilogue(const KgFp8Args& p, v16f (&acc)[BN / 64][BM / 64], int m0, int m_end, int n0, int nt,
+                            int lane, int wn, int arow0, float (*xam)[BM]) {
+  constexpr int TI = BN / 64, TJ = BM / 64;
+  const int half = p.n >> 1;
+  if constexpr (MODE != 2) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int gm = m0 + arow0 + j * 32;
+      if (gm >= m_end) continue;
+      u16* crow = p.c + (size_t)gm * p.ldc;
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int gn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
+          const v16f& v = acc[i][j];
+          if (gn + 3 < p.n) {
+            uint2 o;
+            o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
+            o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
+            *reinterpret_cast<uint2*>(crow + gn) = o;
+          } else {
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+              if (gn + x < p.n) crow[gn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
+          }
+        }
+    }
+  } else {
+    // silu(g) * u in registers: gate tile i pairs with up tile i + TI/2 at the same output columns.
+    // Same arithmetic as the unfused pair (bf16 gate_up, then glm_silu_mul_quant), so results match it
+    // bit for bit.  The product overwrites the gate accumulator, which keeps it out of the VGPR budget.
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      float am = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TI / 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          // the gate_up output is bf16 in the reference (g13), so g and u are rounded before the SiLU
+          const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
+                                           kg_bf16_to_f32(kg_f32_to_bf16(acc[i + TI / 2][j][r])));
+          acc[i][j][r] = v;
+          am = fmaxf(am, fabsf(v));
+        }
+      am = fmaxf(am, __shfl_xor(am, 32, 64));
+      if (lane < 32) xam[wn][arow0 + j * 32] = am;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int lr = arow0 + j * 32, gm = m0 + lr;
+      const float am = fmaxf(xam[0][lr], xam[1][lr]);
+      const u32 e = kg_ue8m0(am, 1e-10f);
+      const float inv = 1.0f / kg_exp2i(e);
+      if (gm >= m_end) continue;
+      u8* qrow = p.q + (size_t)gm * half;
+#pragma unroll
+      for (int i = 0; i < TI / 2; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int cn = n0 + wn * (BN / 4) + i * 32 + rr * 8 + (lane >> 5) * 4;
+          const v16f& a4 = acc[i][j];
+          const float v[4] = {a4[rr * 4], a4[rr * 4 + 1], a4[rr * 4 + 2], a4[rr * 4 + 3]};
+          *reinterpret_cast<u32*>(qrow + cn) = kg_e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+        }
+      if (wn == 0 && lane < 32)
+        p.qsf[((size_t)(nt >> 2) * p.sf_rows + gm) * 4 + (nt & 3)] = (u8)e;
+    }
+  }
 }
 
 template <int BM, int BN, int MODE>
@@ -199,12 +278,19 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   const __amdgpu_buffer_rsrc_t rw = kg_rsrc(p.w + (size_t)g * p.n * p.k, (long long)p.n * p.k);
   const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
   const __amdgpu_buffer_rsrc_t rsb = kg_rsrc(p.sfb + (size_t)g * kw * p.n, (long long)kw * p.n * 4);
-  const int chunk = ((lane & 7) ^ (lane >> 3)) << 4;
-  const unsigned va = (unsigned)((lane >> 3) * p.lda + chunk);
-  const unsigned vw = (unsigned)((lane >> 3) * p.k + chunk);
+  // NQA and NQB are even and every wave starts at an even instruction, so instruction q's rows start at
+  // 8 * (even + q): row r = 8 * (that) + (lane >> 3) has (r >> 1) & 7 = ((q & 1) << 2) | (lane >> 4)
+  static_assert(NQA % 2 == 0 && NQB % 2 == 0, "DMA swizzle parity");
+  unsigned va[2], vw[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = ((lane & 7) ^ ((lane >> 4) | (par << 2))) << 4;
+    va[par] = (unsigned)((lane >> 3) * p.lda + chunk);
+    vw[par] = (unsigned)((lane >> 3) * p.k + chunk);
+  }
 
   // ---- per-lane LDS fragment offsets and scale word offsets.  Every fragment row is (lane & 31) plus a
-  // multiple of 8, so its swizzle is (chunk ^ (lane & 7)) and tile offsets are immediates.
+  // multiple of 32, so its swizzle is (chunk ^ ((lane & 31) >> 1 & 7)) and tile offsets are immediates.
   const int arow0 = wm * (BM / 2) + (lane & 31);               // activation rows: + 32 j
   const int wbase = MODE == 2 ? wn * (BN / 4) : wn * (BN / 2);  // weight rows: + wtile(i)
   auto wtile = [](int i) -> int {
@@ -216,7 +302,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const unsigned sw = (unsigned)(((kh * 4 + (lane >> 5) * 2 + h) ^ (lane & 7)) << 4);
+      const unsigned sw = (unsigned)(((kh * 4 + (lane >> 5) * 2 + h) ^ (((lane & 31) >> 1) & 7)) << 4);
       offa[kh][h] = (unsigned)arow0 * 128u + sw;
       offw[kh][h] = (unsigned)SA + (unsigned)(wbase + (lane & 31)) * 128u + sw;
     }
@@ -257,9 +343,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   do {                                                                                                    \
     const int kg4_ = (KTV) >> 2;                                                                           \
     _Pragma("unroll") for (int j = 0; j < TJ; ++j)                                                         \
-      XA[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, kg4_ * p.sfa_rows * 4, 0);        \
+      XA[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128 + kg4_ * p.sfa_rows * 4, 0, 0);    \
     _Pragma("unroll") for (int i = 0; i < TI; ++i)                                                         \
-      XB[i] = __builtin_amdgcn_raw_buffer_load_b32(rsb, sb_off[i], kg4_ * p.n * 4, 0);                      \
+      XB[i] = __builtin_amdgcn_raw_buffer_load_b32(rsb, sb_off[i] + kg4_ * p.n * 4, 0, 0);                  \
   } while (0)
   // fragment of operand row x (outer if O, else inner) of K half kh from a stage
 #define KG_FRAG_W(ST, KH, I) kg_lds_frag((ST) + wtile(I) * 128, offw[KH][0], offw[KH][1])
@@ -348,84 +434,380 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 
   // ---- epilogue
   kg_mfma_drain();
-  if constexpr (MODE != 2) {
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int gm = m0 + arow0 + j * 32;
-      if (gm >= m_end) continue;
-      u16* crow = p.c + (size_t)gm * p.ldc;
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int gn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
-          const v16f& v = acc[i][j];
-          if (gn + 3 < p.n) {
-            uint2 o;
-            o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
-            o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
-            *reinterpret_cast<uint2*>(crow + gn) = o;
-          } else {
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-              if (gn + x < p.n) crow[gn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
-          }
-        }
-    }
+  kg_fp8_epilogue<BM, BN, MODE>(p, acc, m0, m_end, n0, nt, lane, wn, arow0, xam);
+}
+
+// ---------------------------------------------------------------- persistent 256 x 256 kernel
+//
+// One workgroup per CU walks output tiles (round r: tile r * gridDim.x + its slot, each full round spread
+// over the XCDs in contiguous chunks).  K advances in sub-steps of 64 through a ring of four LDS stages of
+// 32 KB (256 A rows + 256 W rows of 64 bytes), each its own __shared__ array.  The DMA of sub-step s + 4
+// is issued right after the barrier of sub-step s, so a copy has three sub-steps (48 MFMAs per wave) to
+// land, and the ring runs on across tiles: the next tile's first four sub-steps and its first scale words
+// are in flight while this tile's epilogue runs.
+//
+// LDS rows are 64 bytes; 16-byte chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 rows of a
+// ds_read_b128 phase cover the 64 banks once and a DMA instruction (16 rows, lanes row-major) needs one
+// lane offset.
+//
+// Bounds: a buffer load's range check covers its VGPR offset only, so every row offset goes into the VGPR
+// offset and only the K offset into the scalar one (it stays inside the row).  A rows past the tile are
+// the next rows of the buffer or zeros past it; W rows past n read zeros; their outputs are not stored.
+// K per tile is padded to a multiple of 512 (eight sub-steps): a padded sub-step reads zeros (null
+// resource) with unit scales.
+
+struct KgPTile {                      // one tile (wave-uniform)
+  int m0, m_end, nt, g;
+};
+
+// Tile idx (< live) -> its rows, column tile and expert.
+template <int MODE>
+KG_DEV KgPTile kg_ptile(const KgFp8Args& p, const int* tp, const int* ps, int total, int idx) {
+  constexpr int G = 8;
+  KgPTile t;
+  if constexpr (MODE == 0) {
+    const int gsz = G * p.n_tiles, grp = idx / gsz, first = grp * G;
+    const int gm = min(p.m_tiles - first, G), r = idx - grp * gsz;
+    t.g = 0;
+    t.nt = r / gm;
+    t.m0 = (first + r % gm) * 256;
+    t.m_end = min(p.m, t.m0 + 256);
   } else {
-    // silu(g) * u in registers: gate tile i pairs with up tile i + TI/2 at the same output columns.
-    // Same arithmetic as the unfused pair (bf16 gate_up, then glm_silu_mul_quant), so results match it
-    // bit for bit.  The product overwrites the gate accumulator, which keeps it out of the VGPR budget.
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      float am = 0.0f;
-#pragma unroll
-      for (int i = 0; i < TI / 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          // the gate_up output is bf16 in the reference (g13), so g and u are rounded before the SiLU
-          const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
-                                           kg_bf16_to_f32(kg_f32_to_bf16(acc[i + TI / 2][j][r])));
-          acc[i][j][r] = v;
-          am = fmaxf(am, fabsf(v));
-        }
-      am = fmaxf(am, __shfl_xor(am, 32, 64));
-      if (lane < 32) xam[wn][arow0 + j * 32] = am;
+    const int rt_flat = idx / p.n_tiles;
+    int lo = 0, hi = p.groups - 1;             // the last g with tp[g] <= rt_flat (it has R_g > 0)
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tp[mid] <= rt_flat) lo = mid; else hi = mid - 1;
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int lr = arow0 + j * 32, gm = m0 + lr;
-      const float am = fmaxf(xam[0][lr], xam[1][lr]);
-      const u32 e = kg_ue8m0(am, 1e-10f);
-      const float inv = 1.0f / kg_exp2i(e);
-      if (gm >= m_end) continue;
-      u8* qrow = p.q + (size_t)gm * half;
-#pragma unroll
-      for (int i = 0; i < TI / 2; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int cn = n0 + wn * (BN / 4) + i * 32 + rr * 8 + (lane >> 5) * 4;
-          const v16f& a4 = acc[i][j];
-          const float v[4] = {a4[rr * 4], a4[rr * 4 + 1], a4[rr * 4 + 2], a4[rr * 4 + 3]};
-          *reinterpret_cast<u32*>(qrow + cn) = kg_e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-        }
-      if (wn == 0 && lane < 32)
-        p.qsf[((size_t)(nt >> 2) * p.sf_rows + gm) * 4 + (nt & 3)] = (u8)e;
-    }
+    const int g = lo;
+    const int rg = (g + 1 < p.groups ? tp[g + 1] : total) - tp[g];
+    const int l = idx - tp[g] * p.n_tiles, grp = l / (G * p.n_tiles);
+    const int gm = min(rg - grp * G, G), r = l - grp * G * p.n_tiles;
+    const int start = g ? ((ps[g - 1] + 127) >> 7) << 7 : 0;
+    const int m0 = start + (grp * G + r % gm) * 256;
+    // values read from LDS are per-lane to the compiler: make them uniform (scalar registers)
+    t.g = __builtin_amdgcn_readfirstlane(g);
+    t.nt = __builtin_amdgcn_readfirstlane(r / gm);
+    t.m0 = __builtin_amdgcn_readfirstlane(m0);
+    t.m_end = __builtin_amdgcn_readfirstlane(min(min(ps[g], p.rows), m0 + 256));
   }
+  return t;
+}
+
+// Where a tile's operands start: A rows from m0 (VGPR offset base), the expert's W panel (resource) and
+// the column tile's first W row (VGPR offset base).  Branch-free: an empty range stands for "no tile".
+struct KgDmaSrc {
+  __amdgpu_buffer_rsrc_t rw;
+  unsigned abase, wbase;
+  int ok;                                      // 0: no tile (loads read zeros)
+};
+
+KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
+  KgDmaSrc d;
+  d.ok = t.g >= 0;
+  d.rw = kg_rsrc(p.w + (size_t)(t.g > 0 ? t.g : 0) * p.n * p.k, d.ok ? (long long)p.n * p.k : 0);
+  d.abase = (unsigned)(t.m0 * p.lda);
+  d.wbase = (unsigned)(t.nt * cn * p.k);
+  return d;
+}
+
+// Round r of this workgroup: the tile it owns, or -1.
+KG_DEV int kg_round_tile(int r, int live) {
+  const int G = (int)gridDim.x, base = r * G, b = (int)blockIdx.x;
+  if (base + G <= live) return base + kg_xcd_remap(b, G);
+  return base + b < live ? base + b : -1;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args p) {
+  constexpr int BM = 256, BN = 256, TI = 4, TJ = 4, NO = 4, NI = 4, SA = 256 * 64, STAGE = 512 * 64;
+  constexpr int BAR = (NO - 2) * NI + 1;      // MFMA slot after which a sub-step's barrier sits
+  constexpr int NSLOT = NO * NI - 1 - BAR;    // slots after it
+  constexpr int CN = MODE == 2 ? 128 : 256;   // output columns (of n) per column tile
+  __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
+  __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) u8 st2[STAGE];
+  __shared__ __attribute__((aligned(1024))) u8 st3[STAGE];
+  __shared__ int ps[MODE == 0 ? 1 : 1024], tp[MODE == 0 ? 1 : 1024], wtot[4];
+  __shared__ float xam[2][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // ---- the live tiles
+  int total = 0, live;
+  if constexpr (MODE == 0) {
+    live = p.m_tiles * p.n_tiles;
+  } else {
+    // expert g owns rows [start_g, psum[g]), start_g = round_up128(psum[g-1]), in R_g = ceil(rows_g / 256)
+    // row tiles; tp[] is the exclusive prefix of R_g (each thread sums four experts, wave shuffles and the
+    // four wave totals complete the scan)
+    int part = 0, tl[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int e = tid * 4 + x;
+      int t = 0;
+      if (e < p.groups) {
+        const int end = p.psum[e];
+        const int start = e ? ((p.psum[e - 1] + 127) >> 7) << 7 : 0;
+        ps[e] = end;
+        t = end > start ? (end - start + BM - 1) / BM : 0;
+      }
+      tl[x] = t;
+      part += t;
+    }
+    int incl = part;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    int base = incl - part;
+    for (int v = 0; v < wave; ++v) base += wtot[v];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int e = tid * 4 + x;
+      if (e < p.groups) tp[e] = base;
+      base += tl[x];
+    }
+    // LDS values are per-lane to the compiler: the tile count is uniform, and the loops depend on it
+    total = __builtin_amdgcn_readfirstlane(wtot[0] + wtot[1] + wtot[2] + wtot[3]);
+    __syncthreads();
+    live = total * p.n_tiles;
+  }
+  int round = 0;
+  const int idx = kg_round_tile(round, live);
+  if (idx < 0) return;                         // uniform
+
+  const int KS = ((p.k + 511) >> 9) << 3;      // sub-steps per tile (padded to a multiple of 8)
+  const int KB = p.k >> 7;                     // live K blocks of 128
+  const int half = p.n >> 1, kw = (p.k + 511) >> 9;
+  const __amdgpu_buffer_rsrc_t rnull = kg_rsrc(p.a, 0);
+  const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a, (long long)p.rows * p.lda);
+  const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
+
+  // per-lane DMA offsets: instruction q of this wave covers rows 16 (4 wave + q) .. + 15 of the tile
+  const int dchunk = ((lane & 3) ^ ((lane >> 4) & 3)) << 4;
+  unsigned va[4], vw[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (wave * 4 + q) * 16 + (lane >> 2);
+    va[q] = (unsigned)(r * p.lda + dchunk);
+    vw[q] = (unsigned)(kg_wrow<MODE, 256>(0, half, r) * p.k + dchunk);
+  }
+  // per-lane fragment offsets (every fragment row is (lane & 31) plus a multiple of 32)
+  const int arow0 = wm * (BM / 2) + (lane & 31);
+  const int wbase = MODE == 2 ? wn * (BN / 4) : wn * (BN / 2);
+  auto wtile = [](int i) -> int {
+    if constexpr (MODE == 2) return i < TI / 2 ? i * 32 : BN / 2 + (i - TI / 2) * 32;
+    else return i * 32;
+  };
+  unsigned offa[2], offw[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const unsigned sw = (unsigned)((((lane >> 5) * 2 + h) ^ (((lane & 31) >> 2) & 3)) << 4);
+    offa[h] = (unsigned)arow0 * 64u + sw;
+    offw[h] = (unsigned)SA + (unsigned)(wbase + (lane & 31)) * 64u + sw;
+  }
+
+  auto dsrc = [&](const KgPTile& t) { return kg_dma_src(p, t, CN); };
+  // DMA instruction q (0..3: A rows 16 (4 wave + q) .., 4..7: the same W rows) of the sub-step at K offset
+  // ko into stage st; past K, or with no tile, it reads zeros
+  auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
+    const bool in = ko < p.k && d.ok;
+    if (q < 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? ra : rnull, (KG_LDS void*)(st + (wave * 4 + q) * 1024), 16,
+                                               va[q] + d.abase, ko, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? d.rw : rnull, (KG_LDS void*)(st + SA + (wave * 4 + q - 4) * 1024),
+                                               16, vw[q - 4] + d.wbase, ko, 0, 0);
+  };
+  // Scale words of word row kg4 (the exponent bytes of K blocks 4 kg4 .. 4 kg4 + 3, byte kb & 3) of tile t;
+  // the MFMA picks its byte with op_sel.  wa/wb[0] is the word group in use, [1] the next one, loaded four
+  // sub-steps before it is needed.
+  u32 wa[2][TJ], wb[2][TI];
+  auto words = [&](const KgPTile& t, int kg4, u32* xa, u32* xb) {
+    const __amdgpu_buffer_rsrc_t rsb =
+        kg_rsrc(p.sfb + (size_t)(t.g > 0 ? t.g : 0) * kw * p.n, t.g >= 0 ? (long long)kw * p.n * 4 : 0);
+    const unsigned sa_off = (unsigned)((t.m0 + arow0) * 4 + kg4 * p.sfa_rows * 4);
+    const int n0 = t.nt * CN;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) xa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, 0, 0);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+      xb[i] = __builtin_amdgcn_raw_buffer_load_b32(
+          rsb, (unsigned)(kg_wrow<MODE, 256>(n0, half, wbase + wtile(i) + (lane & 31)) * 4 + kg4 * p.n * 4), 0, 0);
+  };
+
+  v16f acc[TI][TJ];
+  v8i res[2][NI], str[2];
+
+#define KG_PFRAG_W(ST, I) kg_lds_frag((ST) + wtile(I) * 64, offw[0], offw[1])
+#define KG_PFRAG_A(ST, J) kg_lds_frag((ST) + (J) * 2048, offa[0], offa[1])
+  // The waits count on the issue order of the DMA and word loads: neither the IR passes nor the scheduler
+  // may swap them.
+#define KG_ISSUE_ORDER()                                                                                   \
+  do {                                                                                                    \
+    asm volatile("" ::: "memory");                                                                        \
+    __builtin_amdgcn_sched_barrier(0);                                                                    \
+  } while (0)
+  // One sub-step s (PH = its index in the group of eight; K block PH / 2 of the word group): 16 MFMAs of
+  // K 64 from stage CUR.  Every other MFMA slot issues one DMA instruction of sub-step s + 3 into PRV, the
+  // stage of sub-step s - 1, which every wave finished reading before the previous barrier; spreading the
+  // eight instructions keeps the vector-memory queue from stalling the MFMA issue.  The barrier after
+  // slot BAR waits for this wave's DMA of sub-step s + 1 and publishes it; the slots after it read NXT's
+  // first fragments.  PH 4 first issues the next word group's 8 loads.  Loads issued after the DMA of
+  // s + 1 (the last of sub-step s - 2) when the barrier waits: sub-step s - 1's 8, this sub-step's 5 up to
+  // slot BAR, and the 8 words if PH 4 is s - 1 or s: 21 on PH 4, 5, else 13.  The last group's sub-steps
+  // 5..7 load the next tile's first three (dsn), as its PH 4 loads the next tile's first word group.
+#define KG_PSUB(CUR, NXT, PRV, PH)                                                                         \
+  do {                                                                                                    \
+    if constexpr ((PH) == 4) {                                                                             \
+      words(wt, wkg, wa[1], wb[1]);                                                                        \
+      KG_ISSUE_ORDER();                                                                                   \
+    }                                                                                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                                    \
+    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
+      _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                     \
+        acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[(PH) & 1][n], acc[o][n], \
+                                                                    0, 0, (PH) >> 1, (int)wb[0][o],       \
+                                                                    (PH) >> 1, (int)wa[0][n]);            \
+        const int slot_ = o * NI + n;                                                                      \
+        if (slot_ % 2 == 0) {                                                                             \
+          if constexpr ((PH) < 5) dma1(PRV, dsc, (ks + (PH) + 3) * 64, slot_ / 2);                          \
+          else dma1(PRV, dsn, dko + ((PH) - 5) * 64, slot_ / 2);                                           \
+        }                                                                                                 \
+        if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, o + 1);                               \
+        if (slot_ == BAR) {                                                                               \
+          if constexpr ((PH) == 4 || (PH) == 5)                                                            \
+            asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else                                                                                            \
+            asm volatile("s_waitcnt vmcnt(13) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+        } else if (slot_ > BAR) {                                                                         \
+          _Pragma("unroll") for (int u = 0; u < NI + 1; ++u) {                                             \
+            if (u * NSLOT / (NI + 1) != slot_ - BAR - 1) continue;                                         \
+            if (u < NI) res[((PH) + 1) & 1][u] = KG_PFRAG_A(NXT, u);                                       \
+            else str[0] = KG_PFRAG_W(NXT, 0);                                                              \
+          }                                                                                               \
+        }                                                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+      }                                                                                                   \
+    }                                                                                                     \
+  } while (0)
+
+  KgPTile cur = kg_ptile<MODE>(p, tp, ps, total, idx);
+  int nidx = kg_round_tile(round + 1, live);
+  // the next tile (g = -1 when there is none: its loads read zeros)
+  KgPTile nxt = cur;
+  nxt.g = -1;
+  if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
+
+  // ---- prologue: the first word group, then sub-steps 0..2 of the first tile in flight (sub-step 0's
+  // slots issue sub-step 3, as in the ring), then sub-step 0's fragments
+  KgDmaSrc dsc = dsrc(cur), dsn = dsrc(nxt);
+  words(cur, 0, wa[0], wb[0]);
+  KG_ISSUE_ORDER();
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    u8* const st = d == 0 ? st0 : d == 1 ? st1 : st2;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) dma1(st, dsc, d * 64, q);
+    KG_ISSUE_ORDER();
+  }
+  asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  str[0] = KG_PFRAG_W(st0, 0);
+#pragma unroll
+  for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, n);
+
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int ks = 0; ks < KS; ks += 8) {
+      // blocks of this word group at or past K (K % 512 != 0) get the unit exponent 127
+      const int live_b = KB - (ks >> 1);
+      if (live_b < 4) {
+        const u32 keep = live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | (0x7f7f7f7fu & ~keep);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | (0x7f7f7f7fu & ~keep);
+      }
+      // the last group hands the ring over to the next tile: its first word group on PH 4 and its first
+      // three sub-steps on PH 5..7
+      const bool lastg = ks + 8 >= KS;
+      const KgPTile wt = lastg ? nxt : cur;
+      const int dko = lastg ? 0 : (ks + 8) * 64, wkg = lastg ? 0 : (ks >> 3) + 1;
+      dsn = dsrc(wt);
+      KG_PSUB(st0, st1, st3, 0);
+      KG_PSUB(st1, st2, st0, 1);
+      KG_PSUB(st2, st3, st1, 2);
+      KG_PSUB(st3, st0, st2, 3);
+      KG_PSUB(st0, st1, st3, 4);
+      KG_PSUB(st1, st2, st0, 5);
+      KG_PSUB(st2, st3, st1, 6);
+      KG_PSUB(st3, st0, st2, 7);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i];
+    }
+    kg_mfma_drain();
+    kg_fp8_epilogue<BM, BN, MODE>(p, acc, cur.m0, cur.m_end, cur.nt * CN, cur.nt, lane, wn, arow0, xam);
+    // the epilogue's stores are vector-memory ops too: settle the count before the ring's waits resume
+    __builtin_amdgcn_s_waitcnt(0);
+    if (nidx < 0) break;
+    ++round;
+    cur = nxt;
+    dsc = dsrc(cur);
+    nidx = kg_round_tile(round + 1, live);
+    nxt.g = -1;
+    if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
+  }
+#undef KG_PSUB
+#undef KG_ISSUE_ORDER
+#undef KG_PFRAG_A
+#undef KG_PFRAG_W
 }
 
 // ---------------------------------------------------------------- host entry points
 
-template __global__ void kg_fp8_gemm_kernel<256, 256, 0>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_kernel<128, 128, 0>(const KgFp8Args);
-template __global__ void kg_fp8_gemm_kernel<256, 256, 1>(const KgFp8Args);
-template __global__ void kg_fp8_gemm_kernel<256, 256, 2>(const KgFp8Args);
+template __global__ void kg_fp8_gemm_persistent<0>(const KgFp8Args);
+template __global__ void kg_fp8_gemm_persistent<1>(const KgFp8Args);
+template __global__ void kg_fp8_gemm_persistent<2>(const KgFp8Args);
 
 template <int BM, int BN, int MODE>
 static int kg_fp8_launch(KgFp8Args& p, int total, hipStream_t st) {
   hipLaunchKernelGGL((kg_fp8_gemm_kernel<BM, BN, MODE>), dim3(total), dim3(256), 0, st, p);
+  return (int)hipGetLastError();
+}
+
+// Compute units of the current device (one persistent workgroup each), cached per device.
+static int kg_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+// The persistent kernel over `tiles` (an upper bound of the live 256 x 256 tiles).
+template <int MODE>
+static int kg_fp8_launch_persistent(KgFp8Args& p, long long tiles, hipStream_t st) {
+  const int grid = (int)(tiles < kg_cu_count() ? tiles : kg_cu_count());
+  if (grid <= 0) return 0;
+  hipLaunchKernelGGL((kg_fp8_gemm_persistent<MODE>), dim3(grid), dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
@@ -443,8 +825,8 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
   const long long big = (long long)((m + 255) / 256) * ((n + 255) / 256);
   if (big >= 256) {
     p.m_tiles = (m + 255) / 256, p.n_tiles = (n + 255) / 256;
-    KG_CHECK(big < (1ll << 31));
-    return kg_fp8_launch<256, 256, 0>(p, (int)big, st);
+    KG_CHECK(big < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+    return kg_fp8_launch_persistent<0>(p, big, st);
   }
   p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
   return kg_fp8_launch<128, 128, 0>(p, p.m_tiles * p.n_tiles, st);
@@ -464,8 +846,8 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
   p.groups = groups;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n + 255) / 256;   // an upper bound of the live tiles
   const long long total = (long long)p.m_tiles * p.n_tiles;
-  KG_CHECK(total < (1ll << 31));
-  return kg_fp8_launch<256, 256, 1>(p, (int)total, (hipStream_t)stream);
+  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+  return kg_fp8_launch_persistent<1>(p, total, (hipStream_t)stream);
 }
 
 extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, const void* sfb,
@@ -482,6 +864,6 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   p.ldc = n, p.sfa_rows = sfa_rows, p.groups = groups, p.sf_rows = sf_rows;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n / 2) / 128;
   const long long total = (long long)p.m_tiles * p.n_tiles;
-  KG_CHECK(total < (1ll << 31));
-  return kg_fp8_launch<256, 256, 2>(p, (int)total, (hipStream_t)stream);
+  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+  return kg_fp8_launch_persistent<2>(p, total, (hipStream_t)stream);
 }
