@@ -34,7 +34,8 @@ int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, 
  * (scripts/glm_ops.py:57-78, docstring 58-61; instance source/glm_deepgemm.cu:40-41):
  * for every group g, rows [round_up128(psum[g-1]), psum[g]) of C (psum[-1] = 0) are the dense GEMM of
  * the same rows of A with weight rows [g n, (g+1) n) and scale words [g k/512, (g+1) k/512).  Rows no group
- * owns are left untouched.  psum: device int32 [groups] (glm_moe_psum's output). */
+ * owns are left untouched.  psum: device int32 [groups] (glm_moe_psum's output).  Requires n % 8 == 0,
+ * ldc % 8 == 0, c 16-byte aligned, rows % 128 == 0, k % 128 == 0, lda % 16 == 0. */
 int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, const void* sfb, void* c, const int* psum,
                      int groups, int n, int k, int rows, int lda, int ldc, int sfa_rows, void* stream);
 

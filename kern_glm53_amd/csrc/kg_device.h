@@ -1,10 +1,13 @@
 // Device-side helpers shared by every kernel of the library (gfx950 / CDNA4, wave64).
 //
-// Numerics are chosen to be bit-reproducible: bf16 and e4m3 conversions are integer code with
-// round-to-nearest-even (e4m3 saturating to +-448 as CUDA's __NV_SATFINITE in the reference,
-// source/glm_glue.cu:76-79 and source/glm_prep.cu:69), the UE8M0 exponent follows
-// source/glm_glue.cu:67-74, and kg_exp is the path's own exp (Cody-Waite reduction, degree-7 Taylor
-// polynomial, explicit fused multiply-adds) evaluated the same way on every device.
+// Numerics are chosen to be bit-reproducible: bf16 and e4m3 results are round-to-nearest-even (e4m3
+// saturating to +-448 as CUDA's __NV_SATFINITE in the reference, source/glm_glue.cu:76-79 and
+// source/glm_prep.cu:69), the UE8M0 exponent follows source/glm_glue.cu:67-74, and kg_exp is the path's
+// own exp (Cody-Waite reduction, degree-7 Taylor polynomial, explicit fused multiply-adds) evaluated the
+// same way on every device.  The bf16 and packed e4m3 conversions use gfx950's conversion instructions
+// (v_cvt_pk_bf16_f32, v_cvt_pk_fp8_f32); on a GPU they give the integer rounding below (kg_e4m3) bit for bit
+// on every non-NaN input (bf16: all ties of every bf16 value and 4M random patterns; e4m3: every bf16 value
+// times powers of two within +-448, the only inputs the path produces, as its block scales bound them).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -21,17 +24,15 @@ KG_DEV u32 kg_f2u(float f) { return __float_as_uint(f); }
 
 KG_DEV float kg_bf16_to_f32(u16 h) { return kg_u2f((u32)h << 16); }
 
-// f32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
-KG_DEV u16 kg_f32_to_bf16(float f) {
-  u32 u = kg_f2u(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
+typedef __bf16 kg_bf16x2 __attribute__((ext_vector_type(2)));
 
-// Two f32 -> packed bf16 pair (lo in bits 0-15).
+// f32 -> bf16 bits, round to nearest even (NaN -> a quiet NaN).
+KG_DEV u16 kg_f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
+
+// Two f32 -> packed bf16 pair (lo in bits 0-15): one v_cvt_pk_bf16_f32.
 KG_DEV u32 kg_pack_bf16x2(float lo, float hi) {
-  return (u32)kg_f32_to_bf16(lo) | ((u32)kg_f32_to_bf16(hi) << 16);
+  const kg_bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(u32, v);
 }
 
 // f32 -> OCP e4m3fn, round to nearest even, saturating to +-448, NaN -> 0x7f | sign.
@@ -53,8 +54,11 @@ KG_DEV u32 kg_e4m3(float x) {
   return sign | r;
 }
 
+// Four f32 within +-448 -> packed e4m3 (a in bits 0-7): two v_cvt_pk_fp8_f32, equal to kg_e4m3 on them.
 KG_DEV u32 kg_e4m3x4(float a, float b, float c, float d) {
-  return kg_e4m3(a) | (kg_e4m3(b) << 8) | (kg_e4m3(c) << 16) | (kg_e4m3(d) << 24);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (u32)w;
 }
 
 // OCP e4m3fn -> f32 (exact).

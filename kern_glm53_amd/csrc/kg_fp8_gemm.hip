@@ -511,6 +511,57 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
   return d;
 }
 
+// Epilogue of the persistent kernel for modes 0 and 1: bf16 through LDS, so that each store writes 16
+// contiguous bytes per lane and 16 lanes cover a 256-byte row segment.  Per m tile j (32 rows), each wave
+// stages its 32 x 128 outputs (8 KB) in the ring stage that is idle during the epilogue, split into the
+// two 4 KB pieces this wave's own DMA writes (so no other wave's DMA into that stage can overlap them).
+// Rows are 256 bytes; chunk c (8 columns) of row m sits in slot c ^ (m & 15), with its two 8-byte halves
+// swapped when m & 16, which makes the 8-byte writes of a wave's 32 rows conflict-free.
+KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int wave, int m0, int m_end,
+                                int n0, int wm, int wn) {
+  // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
+  // tile, rather than hoisted out of the tile loop into registers the K loop needs.
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  const __amdgpu_buffer_rsrc_t rc = kg_rsrc(p.c, (long long)p.rows * p.ldc * 2);
+  u8* const lo = stage + wave * 4096;            // rows 0..15 of the wave's staging
+  u8* const hi = stage + 256 * 64 + wave * 4096;  // rows 16..31
+  const int mr = lane & 31;                       // this lane's row when writing
+  u8* const wrow = (mr < 16 ? lo : hi) + (mr & 15) * 256;
+  const int hsel = (lane >> 5) ^ ((lane >> 4) & 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int c = i * 4 + rr;
+        uint2 o;
+        o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+        o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+        *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4) + (hsel << 3)) = o;
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's writes are in LDS
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int idx = t * 64 + lane, m = idx >> 4, c = idx & 15;
+      const u8* rrow = (m < 16 ? lo : hi) + (m & 15) * 256;
+      uint4 v = *reinterpret_cast<const uint4*>(rrow + ((c ^ (m & 15)) << 4));
+      if (m & 16) {
+        const unsigned x = v.x, y = v.y;
+        v.x = v.z, v.y = v.w, v.z = x, v.w = y;
+      }
+      const int gm = m0 + wm * 128 + j * 32 + m, gn = n0 + wn * 128 + c * 8;
+      // always issued (a fixed count of 32 stores per wave and tile, which the K loop's waits count on);
+      // lanes outside the tile's rows or columns get an offset past the resource, which drops the write
+      const unsigned off = gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
+      __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
+      __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);           // reads done before the next m tile's writes
+  }
+}
+
 // Round r of this workgroup: the tile it owns, or -1.
 KG_DEV int kg_round_tile(int r, int live) {
   const int G = (int)gridDim.x, base = r * G, b = (int)blockIdx.x;
@@ -659,7 +710,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // stage of sub-step s - 1, which every wave finished reading before the previous barrier; spreading the
   // eight instructions keeps the vector-memory queue from stalling the MFMA issue.  The barrier after
   // slot BAR waits for this wave's DMA of sub-step s + 1 and publishes it; the slots after it read NXT's
-  // first fragments.  PH 4 first issues the next word group's 8 loads.  Loads issued after the DMA of
+  // first fragments.  PH 4 first issues the next word group's 8 loads.  After a modes-0/1 epilogue its
+  // 32 stores (issued after the DMA of the tile's sub-steps 1 and 2) are still in flight at the barriers of
+  // the tile's sub-steps 0 and 1, which then count 45.  Loads issued after the DMA of
   // s + 1 (the last of sub-step s - 2) when the barrier waits: sub-step s - 1's 8, this sub-step's 5 up to
   // slot BAR, and the 8 words if PH 4 is s - 1 or s: 21 on PH 4, 5, else 13.  The last group's sub-steps
   // 5..7 load the next tile's first three (dsn), as its PH 4 loads the next tile's first word group.
@@ -684,6 +737,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
         if (slot_ == BAR) {                                                                               \
           if constexpr ((PH) == 4 || (PH) == 5)                                                            \
             asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else if ((PH) <= 1 && ks == 0 && stores_pending)                                                 \
+            asm volatile("s_waitcnt vmcnt(45) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
           else                                                                                            \
             asm volatile("s_waitcnt vmcnt(13) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
         } else if (slot_ > BAR) {                                                                         \
@@ -722,6 +777,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
   for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, n);
 
+  bool stores_pending = false;
   for (;;) {
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -759,9 +815,14 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
       for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i];
     }
     kg_mfma_drain();
-    kg_fp8_epilogue<BM, BN, MODE>(p, acc, cur.m0, cur.m_end, cur.nt * CN, cur.nt, lane, wn, arow0, xam);
-    // the epilogue's stores are vector-memory ops too: settle the count before the ring's waits resume
-    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (MODE == 2)
+      kg_fp8_epilogue<BM, BN, MODE>(p, acc, cur.m0, cur.m_end, cur.nt * CN, cur.nt, lane, wn, arow0, xam);
+    else   // stage 3 is idle until the next tile's first sub-step issues its DMA
+      kg_fp8_epilogue_lds(p, acc, st3, wave, cur.m0, cur.m_end, cur.nt * CN, wm, wn);
+    // modes 0/1: the epilogue's 32 stores stay in flight, counted by the next tile's first two barriers;
+    // mode 2 (a data-dependent store count) settles them here
+    if constexpr (MODE == 2) __builtin_amdgcn_s_waitcnt(0);
+    stores_pending = MODE != 2;
     if (nidx < 0) break;
     ++round;
     cur = nxt;
@@ -770,6 +831,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     nxt.g = -1;
     if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
   }
+  __builtin_amdgcn_s_waitcnt(0);
 #undef KG_PSUB
 #undef KG_ISSUE_ORDER
 #undef KG_PFRAG_A
@@ -823,7 +885,8 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
   p.m = m, p.n = n, p.k = k, p.rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows, p.groups = 1;
   hipStream_t st = (hipStream_t)stream;
   const long long big = (long long)((m + 255) / 256) * ((n + 255) / 256);
-  if (big >= 256) {
+  // the persistent kernel's epilogue stores 16-byte chunks of 8 columns
+  if (big >= 256 && n % 8 == 0 && ldc % 8 == 0 && kg_aligned(c, 16) && (long long)rows * ldc * 2 < (1ll << 31)) {
     p.m_tiles = (m + 255) / 256, p.n_tiles = (n + 255) / 256;
     KG_CHECK(big < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
     return kg_fp8_launch_persistent<0>(p, big, st);
@@ -836,9 +899,10 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
                                 const int* psum, int groups, int n, int k, int rows, int lda, int ldc, int sfa_rows,
                                 void* stream) {
   KG_CHECK(a && w && sfa && sfb && c && psum && groups >= 1 && groups <= 1024);
-  KG_CHECK(n > 0 && k > 0 && k % 128 == 0 && rows > 0 && rows % 128 == 0 && rows <= sfa_rows && n <= ldc &&
-           k <= lda);
-  KG_CHECK(lda % 16 == 0 && ldc % 4 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(c, 8));
+  KG_CHECK(n > 0 && n % 8 == 0 && k > 0 && k % 128 == 0 && rows > 0 && rows % 128 == 0 && rows <= sfa_rows &&
+           n <= ldc && k <= lda);
+  KG_CHECK(lda % 16 == 0 && ldc % 8 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(c, 16));
+  KG_CHECK((long long)rows * ldc * 2 < (1ll << 31));
   KG_CHECK(kg_aligned(sfa, 4) && kg_aligned(sfb, 4));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
