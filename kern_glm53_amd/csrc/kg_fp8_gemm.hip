@@ -102,77 +102,33 @@ KG_DEV void kg_fp8_dma(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_
 }
 
 // Epilogue of one BM x BN output tile held in acc (after the K loop and kg_mfma_drain): bf16 stores of the
-// rows [m0, m_end) (modes 0, 1), or the fused SiLU-mul + e4m3 requant of the gate / up column pairs (mode 2).
-template <int BM, int BN, int MODE>
-KG_DEV void kg_fp8_epilogue(const KgFp8Args& p, v16f (&acc)[BN / 64][BM / 64], int m0, int m_end, int n0, int nt,
-                            int lane, int wn, int arow0, float (*xam)[BM]) {
+// rows [m0, m_end) and columns [n0, n).
+template <int BM, int BN>
+KG_DEV void kg_fp8_epilogue(const KgFp8Args& p, v16f (&acc)[BN / 64][BM / 64], int m0, int m_end, int n0,
+                            int lane, int wn, int arow0) {
   constexpr int TI = BN / 64, TJ = BM / 64;
-  const int half = p.n >> 1;
-  if constexpr (MODE != 2) {
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int gm = m0 + arow0 + j * 32;
-      if (gm >= m_end) continue;
-      u16* crow = p.c + (size_t)gm * p.ldc;
+  for (int j = 0; j < TJ; ++j) {
+    const int gm = m0 + arow0 + j * 32;
+    if (gm >= m_end) continue;
+    u16* crow = p.c + (size_t)gm * p.ldc;
 #pragma unroll
-      for (int i = 0; i < TI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int gn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
-          const v16f& v = acc[i][j];
-          if (gn + 3 < p.n) {
-            uint2 o;
-            o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
-            o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
-            *reinterpret_cast<uint2*>(crow + gn) = o;
-          } else {
+      for (int rr = 0; rr < 4; ++rr) {
+        const int gn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
+        const v16f& v = acc[i][j];
+        if (gn + 3 < p.n) {
+          uint2 o;
+          o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(crow + gn) = o;
+        } else {
 #pragma unroll
-            for (int x = 0; x < 4; ++x)
-              if (gn + x < p.n) crow[gn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
-          }
+          for (int x = 0; x < 4; ++x)
+            if (gn + x < p.n) crow[gn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
         }
-    }
-  } else {
-    // silu(g) * u in registers: gate tile i pairs with up tile i + TI/2 at the same output columns.
-    // Same arithmetic as the unfused pair (bf16 gate_up, then glm_silu_mul_quant), so results match it
-    // bit for bit.  The product overwrites the gate accumulator, which keeps it out of the VGPR budget.
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      float am = 0.0f;
-#pragma unroll
-      for (int i = 0; i < TI / 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          // the gate_up output is bf16 in the reference (g13), so g and u are rounded before the SiLU
-          const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
-                                           kg_bf16_to_f32(kg_f32_to_bf16(acc[i + TI / 2][j][r])));
-          acc[i][j][r] = v;
-          am = fmaxf(am, fabsf(v));
-        }
-      am = fmaxf(am, __shfl_xor(am, 32, 64));
-      if (lane < 32) xam[wn][arow0 + j * 32] = am;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int lr = arow0 + j * 32, gm = m0 + lr;
-      const float am = fmaxf(xam[0][lr], xam[1][lr]);
-      const u32 e = kg_ue8m0(am, 1e-10f);
-      const float inv = 1.0f / kg_exp2i(e);
-      if (gm >= m_end) continue;
-      u8* qrow = p.q + (size_t)gm * half;
-#pragma unroll
-      for (int i = 0; i < TI / 2; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int cn = n0 + wn * (BN / 4) + i * 32 + rr * 8 + (lane >> 5) * 4;
-          const v16f& a4 = acc[i][j];
-          const float v[4] = {a4[rr * 4], a4[rr * 4 + 1], a4[rr * 4 + 2], a4[rr * 4 + 3]};
-          *reinterpret_cast<u32*>(qrow + cn) = kg_e4m3x4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
-        }
-      if (wn == 0 && lane < 32)
-        p.qsf[((size_t)(nt >> 2) * p.sf_rows + gm) * 4 + (nt & 3)] = (u8)e;
-    }
+      }
   }
 }
 
@@ -186,7 +142,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
   __shared__ int ps[1024], tp[1024], wtot[4];
-  __shared__ float xam[2][BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -434,7 +389,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 
   // ---- epilogue
   kg_mfma_drain();
-  kg_fp8_epilogue<BM, BN, MODE>(p, acc, m0, m_end, n0, nt, lane, wn, arow0, xam);
+  kg_fp8_epilogue<BM, BN>(p, acc, m0, m_end, n0, lane, wn, arow0);
 }
 
 // ---------------------------------------------------------------- persistent 256 x 256 kernel
@@ -500,6 +455,7 @@ struct KgDmaSrc {
   __amdgpu_buffer_rsrc_t rw;
   unsigned abase, wbase;
   int ok;                                      // 0: no tile (loads read zeros)
+  int half;                                    // a tile of at most 128 rows: A rows 128.. are not loaded
 };
 
 KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
@@ -508,6 +464,7 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
   d.rw = kg_rsrc(p.w + (size_t)(t.g > 0 ? t.g : 0) * p.n * p.k, d.ok ? (long long)p.n * p.k : 0);
   d.abase = (unsigned)(t.m0 * p.lda);
   d.wbase = (unsigned)(t.nt * cn * p.k);
+  d.half = t.m_end - t.m0 <= 128;
   return d;
 }
 
@@ -518,7 +475,7 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 // Rows are 256 bytes; chunk c (8 columns) of row m sits in slot c ^ (m & 15), with its two 8-byte halves
 // swapped when m & 16, which makes the 8-byte writes of a wave's 32 rows conflict-free.
 KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int wave, int m0, int m_end,
-                                int n0, int wm, int wn) {
+                                int n0, int wm, int wn, bool half) {
   // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
   // tile, rather than hoisted out of the tile loop into registers the K loop needs.
   int lane;
@@ -529,37 +486,114 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
   const int mr = lane & 31;                       // this lane's row when writing
   u8* const wrow = (mr < 16 ? lo : hi) + (mr & 15) * 256;
   const int hsel = (lane >> 5) ^ ((lane >> 4) & 1);
+  const int rbase = m0 + (half ? wm * 64 : wm * 128);   // a half tile's waves own 64 rows each
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
+    const bool jv = !half || j < 2;               // a half tile has two m tiles per wave
+    if (jv) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int c = i * 4 + rr;
-        uint2 o;
-        o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
-        o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
-        *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4) + (hsel << 3)) = o;
-      }
-    __builtin_amdgcn_s_waitcnt(0xc07f);           // lgkmcnt(0): this wave's writes are in LDS
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = i * 4 + rr;
+          uint2 o;
+          o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4) + (hsel << 3)) = o;
+        }
+      __builtin_amdgcn_s_waitcnt(0xc07f);         // lgkmcnt(0): this wave's writes are in LDS
+    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int idx = t * 64 + lane, m = idx >> 4, c = idx & 15;
       const u8* rrow = (m < 16 ? lo : hi) + (m & 15) * 256;
-      uint4 v = *reinterpret_cast<const uint4*>(rrow + ((c ^ (m & 15)) << 4));
+      uint4 v = {0u, 0u, 0u, 0u};
+      if (jv) v = *reinterpret_cast<const uint4*>(rrow + ((c ^ (m & 15)) << 4));
       if (m & 16) {
         const unsigned x = v.x, y = v.y;
         v.x = v.z, v.y = v.w, v.z = x, v.w = y;
       }
-      const int gm = m0 + wm * 128 + j * 32 + m, gn = n0 + wn * 128 + c * 8;
+      const int gm = rbase + j * 32 + m, gn = n0 + wn * 128 + c * 8;
       // always issued (a fixed count of 32 stores per wave and tile, which the K loop's waits count on);
       // lanes outside the tile's rows or columns get an offset past the resource, which drops the write
-      const unsigned off = gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
+      const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
       __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
       __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);           // reads done before the next m tile's writes
   }
+}
+
+// Epilogue of the persistent kernel for mode 2 (the fused SiLU-mul + per-128 e4m3 requant).  The tile's
+// 256 weight rows are 128 gate rows and the matching 128 up rows, so a wave's gate accumulators i = 0, 1
+// pair with its up accumulators i + 2 at the same output columns.  Same arithmetic as the unfused pair
+// (bf16 gate_up output, then glm_silu_mul_quant): g and u are rounded to bf16, v = bf16(silu(g) u), the
+// 128-column amax goes through LDS (xam) to the wave holding the other 64 columns of the row.  The e4m3
+// codes of the whole 256 x 128 output tile are staged in LDS (the idle ring stage, row r at r * 128 with
+// 16-byte chunk c in slot c ^ (r & 7)) and then stored a full 128-byte row segment per 8 lanes: every
+// wave issues exactly 8 code stores and 1 exponent-byte store (offsets past the resource drop the rows
+// past the tile), a count the next tile's first barriers wait on.
+KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, float (*xam)[256], u8* xe,
+                                 int wave, int m0, int m_end, int nt, int wm, int wn, bool half) {
+  int lane;   // from a volatile read: keeps the per-lane address math here rather than hoisted
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  const int hn = p.n >> 1;
+  const int arow0 = (half ? wm * 64 : wm * 128) + (lane & 31);   // a half tile's waves own 64 rows each
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (half && j >= 2) continue;
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
+                                         kg_bf16_to_f32(kg_f32_to_bf16(acc[i + 2][j][r])));
+        acc[i][j][r] = v;                        // the product overwrites the gate accumulator
+        am = fmaxf(am, fabsf(v));
+      }
+    am = fmaxf(am, __shfl_xor(am, 32, 64));
+    if (lane < 32) xam[wn][arow0 + j * 32] = am;
+  }
+  // LDS-only barriers: the vector-memory queue (the next tile's DMA in flight) is not waited on
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (half && j >= 2) continue;
+    const int lr = arow0 + j * 32;
+    const float am = fmaxf(xam[0][lr], xam[1][lr]);
+    const u32 e = kg_ue8m0(am, 1e-10f);
+    const float inv = 1.0f / kg_exp2i(e);
+    u8* const srow = stage + lr * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int col = wn * 64 + i * 32 + rr * 8 + (lane >> 5) * 4;   // output column within the tile
+        const v16f& a4 = acc[i][j];
+        *reinterpret_cast<u32*>(srow + ((((col >> 4) ^ (lr & 7)) << 4) | (col & 15))) =
+            kg_e4m3x4(a4[rr * 4] * inv, a4[rr * 4 + 1] * inv, a4[rr * 4 + 2] * inv, a4[rr * 4 + 3] * inv);
+      }
+    if (wn == 0 && lane < 32) xe[lr] = (u8)e;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const __amdgpu_buffer_rsrc_t rq = kg_rsrc(p.q, (long long)p.rows * hn);
+  const __amdgpu_buffer_rsrc_t rs = kg_rsrc(p.qsf, (long long)((hn + 511) >> 9) * p.sf_rows * 4);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int r = wave * 64 + t * 8 + (lane >> 3), c = lane & 7, gm = m0 + r;
+    const uint4 v = *reinterpret_cast<const uint4*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
+    const unsigned off = gm < m_end ? (unsigned)(gm * hn + nt * 128 + c * 16) : 0x80000000u;
+    __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(d4, rq, off, 0, 0);
+  }
+  {
+    const int r = wave * 64 + lane, gm = m0 + r;
+    const unsigned off = gm < m_end ? (unsigned)((((nt >> 2) * p.sf_rows + gm) << 2) + (nt & 3)) : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b8((u8)xe[r], rs, off, 0, 0);
+  }
+  // staging reads done in every wave before the ring's next DMA into the stage; the stores stay in flight
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Round r of this workgroup: the tile it owns, or -1.
@@ -580,7 +614,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   __shared__ __attribute__((aligned(1024))) u8 st2[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st3[STAGE];
   __shared__ int ps[MODE == 0 ? 1 : 1024], tp[MODE == 0 ? 1 : 1024], wtot[4];
-  __shared__ float xam[2][BM];
+  __shared__ float xam[MODE == 2 ? 2 : 1][BM];
+  __shared__ u8 xe[MODE == 2 ? BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -669,9 +704,10 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // ko into stage st; past K, or with no tile, it reads zeros
   auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
     const bool in = ko < p.k && d.ok;
-    if (q < 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? ra : rnull, (KG_LDS void*)(st + (wave * 4 + q) * 1024), 16,
-                                               va[q] + d.abase, ko, 0, 0);
+    if (q < 4)   // (a half tile's rows 128.. read zeros; the instruction is issued all the same)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(in && !(d.half && wave >= 2) ? ra : rnull,
+                                               (KG_LDS void*)(st + (wave * 4 + q) * 1024), 16, va[q] + d.abase, ko,
+                                               0, 0);
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? d.rw : rnull, (KG_LDS void*)(st + SA + (wave * 4 + q - 4) * 1024),
                                                16, vw[q - 4] + d.wbase, ko, 0, 0);
@@ -683,7 +719,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   auto words = [&](const KgPTile& t, int kg4, u32* xa, u32* xb) {
     const __amdgpu_buffer_rsrc_t rsb =
         kg_rsrc(p.sfb + (size_t)(t.g > 0 ? t.g : 0) * kw * p.n, t.g >= 0 ? (long long)kw * p.n * 4 : 0);
-    const unsigned sa_off = (unsigned)((t.m0 + arow0) * 4 + kg4 * p.sfa_rows * 4);
+    const int arow = t.m_end - t.m0 <= 128 ? arow0 - wm * 64 : arow0;   // a half tile's wave rows
+    const unsigned sa_off = (unsigned)((t.m0 + arow) * 4 + kg4 * p.sfa_rows * 4);
     const int n0 = t.nt * CN;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) xa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, 0, 0);
@@ -710,9 +747,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // stage of sub-step s - 1, which every wave finished reading before the previous barrier; spreading the
   // eight instructions keeps the vector-memory queue from stalling the MFMA issue.  The barrier after
   // slot BAR waits for this wave's DMA of sub-step s + 1 and publishes it; the slots after it read NXT's
-  // first fragments.  PH 4 first issues the next word group's 8 loads.  After a modes-0/1 epilogue its
-  // 32 stores (issued after the DMA of the tile's sub-steps 1 and 2) are still in flight at the barriers of
-  // the tile's sub-steps 0 and 1, which then count 45.  Loads issued after the DMA of
+  // first fragments.  PH 4 first issues the next word group's 8 loads.  After an epilogue its stores
+  // (32 in modes 0/1, 9 in mode 2, issued after the DMA of the tile's sub-steps 1 and 2) are still in
+  // flight at the barriers of the tile's sub-steps 0 and 1, which then count 45 (22).  Loads issued after the DMA of
   // s + 1 (the last of sub-step s - 2) when the barrier waits: sub-step s - 1's 8, this sub-step's 5 up to
   // slot BAR, and the 8 words if PH 4 is s - 1 or s: 21 on PH 4, 5, else 13.  The last group's sub-steps
   // 5..7 load the next tile's first three (dsn), as its PH 4 loads the next tile's first word group.
@@ -737,6 +774,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
         if (slot_ == BAR) {                                                                               \
           if constexpr ((PH) == 4 || (PH) == 5)                                                            \
             asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else if ((PH) <= 1 && ks == 0 && stores_pending && MODE == 2)                                    \
+            asm volatile("s_waitcnt vmcnt(22) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
           else if ((PH) <= 1 && ks == 0 && stores_pending)                                                 \
             asm volatile("s_waitcnt vmcnt(45) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
           else                                                                                            \
@@ -745,6 +784,49 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           _Pragma("unroll") for (int u = 0; u < NI + 1; ++u) {                                             \
             if (u * NSLOT / (NI + 1) != slot_ - BAR - 1) continue;                                         \
             if (u < NI) res[((PH) + 1) & 1][u] = KG_PFRAG_A(NXT, u);                                       \
+            else str[0] = KG_PFRAG_W(NXT, 0);                                                              \
+          }                                                                                               \
+        }                                                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+      }                                                                                                   \
+    }                                                                                                     \
+  } while (0)
+
+  // Half tiles (at most 128 rows, an expert's tail): the 4 waves split 2 x 2 over 128 x 256, so a wave
+  // owns rows wm * 64 + 32 j (j < 2) against the same 128 weight rows: 8 MFMAs per sub-step.  The DMA is
+  // the same 8 instructions per sub-step (waves 2, 3 load zeros for A), one per MFMA slot; the barrier
+  // after slot BARH = 5 counts this sub-step's 6, so 14 (22 on PH 4, 5; 46 / 23 after an epilogue).
+  constexpr int NIH = 2, BARH = (NO - 2) * NIH + 1, NSLOTH = NO * NIH - 1 - BARH;
+#define KG_PFRAG_AH(ST, J) kg_lds_frag((ST) + (J) * 2048 - wm * 4096, offa[0], offa[1])
+#define KG_PSUBH(CUR, NXT, PRV, PH)                                                                        \
+  do {                                                                                                    \
+    if constexpr ((PH) == 4) {                                                                             \
+      words(wt, wkg, wa[1], wb[1]);                                                                        \
+      KG_ISSUE_ORDER();                                                                                   \
+    }                                                                                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                                    \
+    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
+      _Pragma("unroll") for (int n = 0; n < NIH; ++n) {                                                    \
+        acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[(PH) & 1][n], acc[o][n], \
+                                                                    0, 0, (PH) >> 1, (int)wb[0][o],       \
+                                                                    (PH) >> 1, (int)wa[0][n]);            \
+        const int slot_ = o * NIH + n;                                                                     \
+        if constexpr ((PH) < 5) dma1(PRV, dsc, (ks + (PH) + 3) * 64, slot_);                                \
+        else dma1(PRV, dsn, dko + ((PH) - 5) * 64, slot_);                                                 \
+        if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, o + 1);                               \
+        if (slot_ == BARH) {                                                                              \
+          if constexpr ((PH) == 4 || (PH) == 5)                                                            \
+            asm volatile("s_waitcnt vmcnt(22) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else if ((PH) <= 1 && ks == 0 && stores_pending && MODE == 2)                                    \
+            asm volatile("s_waitcnt vmcnt(23) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else if ((PH) <= 1 && ks == 0 && stores_pending)                                                 \
+            asm volatile("s_waitcnt vmcnt(46) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+          else                                                                                            \
+            asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
+        } else if (slot_ > BARH) {                                                                        \
+          _Pragma("unroll") for (int u = 0; u < NIH + 1; ++u) {                                            \
+            if (u * NSLOTH / (NIH + 1) != slot_ - BARH - 1) continue;                                      \
+            if (u < NIH) res[((PH) + 1) & 1][u] = KG_PFRAG_AH(NXT, u);                                     \
             else str[0] = KG_PFRAG_W(NXT, 0);                                                              \
           }                                                                                               \
         }                                                                                                 \
@@ -773,56 +855,81 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     KG_ISSUE_ORDER();
   }
   asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  str[0] = KG_PFRAG_W(st0, 0);
-#pragma unroll
-  for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, n);
 
   bool stores_pending = false;
   for (;;) {
+    const bool halft = cur.m_end - cur.m0 <= 128;
+    // sub-step 0's first fragments (stage 0 holds the tile's sub-step 0, published by the last barrier;
+    // read here because the previous tile may have had the other shape)
+    str[0] = KG_PFRAG_W(st0, 0);
+    if (halft) {
+#pragma unroll
+      for (int n = 0; n < NIH; ++n) res[0][n] = KG_PFRAG_AH(st0, n);
+    } else {
+#pragma unroll
+      for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, n);
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    for (int ks = 0; ks < KS; ks += 8) {
-      // blocks of this word group at or past K (K % 512 != 0) get the unit exponent 127
-      const int live_b = KB - (ks >> 1);
-      if (live_b < 4) {
-        const u32 keep = live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | (0x7f7f7f7fu & ~keep);
-#pragma unroll
-        for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | (0x7f7f7f7fu & ~keep);
+    // per group of eight sub-steps: blocks of the word group at or past K (K % 512 != 0) get the unit
+    // exponent 127; the last group hands the ring over to the next tile (its first word group on PH 4, its
+    // first three sub-steps on PH 5..7)
+#define KG_GROUP_START()                                                                                   \
+  const int live_b = KB - (ks >> 1);                                                                        \
+  if (live_b < 4) {                                                                                        \
+    const u32 keep = live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));                               \
+    _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | (0x7f7f7f7fu & ~keep);   \
+    _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | (0x7f7f7f7fu & ~keep);   \
+  }                                                                                                        \
+  const bool lastg = ks + 8 >= KS;                                                                         \
+  const KgPTile wt = lastg ? nxt : cur;                                                                    \
+  const int dko = lastg ? 0 : (ks + 8) * 64, wkg = lastg ? 0 : (ks >> 3) + 1;                              \
+  dsn = dsrc(wt)
+#define KG_GROUP_END()                                                                                     \
+  _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
+  _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i]
+    if (halft) {
+      for (int ks = 0; ks < KS; ks += 8) {
+        KG_GROUP_START();
+        KG_PSUBH(st0, st1, st3, 0);
+        KG_PSUBH(st1, st2, st0, 1);
+        KG_PSUBH(st2, st3, st1, 2);
+        KG_PSUBH(st3, st0, st2, 3);
+        KG_PSUBH(st0, st1, st3, 4);
+        KG_PSUBH(st1, st2, st0, 5);
+        KG_PSUBH(st2, st3, st1, 6);
+        KG_PSUBH(st3, st0, st2, 7);
+        KG_GROUP_END();
       }
-      // the last group hands the ring over to the next tile: its first word group on PH 4 and its first
-      // three sub-steps on PH 5..7
-      const bool lastg = ks + 8 >= KS;
-      const KgPTile wt = lastg ? nxt : cur;
-      const int dko = lastg ? 0 : (ks + 8) * 64, wkg = lastg ? 0 : (ks >> 3) + 1;
-      dsn = dsrc(wt);
-      KG_PSUB(st0, st1, st3, 0);
-      KG_PSUB(st1, st2, st0, 1);
-      KG_PSUB(st2, st3, st1, 2);
-      KG_PSUB(st3, st0, st2, 3);
-      KG_PSUB(st0, st1, st3, 4);
-      KG_PSUB(st1, st2, st0, 5);
-      KG_PSUB(st2, st3, st1, 6);
-      KG_PSUB(st3, st0, st2, 7);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];
-#pragma unroll
-      for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i];
+    } else {
+      for (int ks = 0; ks < KS; ks += 8) {
+        KG_GROUP_START();
+        KG_PSUB(st0, st1, st3, 0);
+        KG_PSUB(st1, st2, st0, 1);
+        KG_PSUB(st2, st3, st1, 2);
+        KG_PSUB(st3, st0, st2, 3);
+        KG_PSUB(st0, st1, st3, 4);
+        KG_PSUB(st1, st2, st0, 5);
+        KG_PSUB(st2, st3, st1, 6);
+        KG_PSUB(st3, st0, st2, 7);
+        KG_GROUP_END();
+      }
     }
+#undef KG_GROUP_START
+#undef KG_GROUP_END
     kg_mfma_drain();
+    // stage 3 is idle until the next tile's first sub-step issues its DMA
     if constexpr (MODE == 2)
-      kg_fp8_epilogue<BM, BN, MODE>(p, acc, cur.m0, cur.m_end, cur.nt * CN, cur.nt, lane, wn, arow0, xam);
-    else   // stage 3 is idle until the next tile's first sub-step issues its DMA
-      kg_fp8_epilogue_lds(p, acc, st3, wave, cur.m0, cur.m_end, cur.nt * CN, wm, wn);
-    // modes 0/1: the epilogue's 32 stores stay in flight, counted by the next tile's first two barriers;
-    // mode 2 (a data-dependent store count) settles them here
-    if constexpr (MODE == 2) __builtin_amdgcn_s_waitcnt(0);
-    stores_pending = MODE != 2;
+      kg_fp8_epilogue_silu(p, acc, st3, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
+    else
+      kg_fp8_epilogue_lds(p, acc, st3, wave, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
+    // the epilogue's stores (32, or 9 in mode 2, per wave) stay in flight, counted by the next tile's
+    // first two barriers
+    stores_pending = true;
     if (nidx < 0) break;
     ++round;
     cur = nxt;
@@ -833,6 +940,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   }
   __builtin_amdgcn_s_waitcnt(0);
 #undef KG_PSUB
+#undef KG_PSUBH
+#undef KG_PFRAG_AH
 #undef KG_ISSUE_ORDER
 #undef KG_PFRAG_A
 #undef KG_PFRAG_W

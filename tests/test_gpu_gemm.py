@@ -57,6 +57,7 @@ def check(out_bits, ref32, abs_sum, k, what, window=None):
     (300, 2624, 1024, 320, 1152, 2752, 384),        # N tail of 64 (2624 = 20.5 x 128), ldc > n, lda > k
     (4096, 4096, 512, 4096, 512, 4096, 4096),       # 256 x 256 tiles
     (4000, 4160, 640, 4096, 640, 4224, 4096),       # 256 x 256 tiles, M and N tails, odd K-block count
+    (4100, 4096, 1536, 4224, 1536, 4096, 4224),     # an M tail of 4 rows (half tiles), K = 3 x 512
     (512, 256, 384, 512, 384, 256, 512),            # odd K-block count, 128 x 128 tiles
     (1, 2048, 6144, 16, 6144, 2048, 16),            # a single row
 ])
