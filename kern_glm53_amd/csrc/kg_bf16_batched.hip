@@ -124,37 +124,43 @@ __global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Arg
   if (kt < KT) compute(st0);
   kg_mfma_drain();
 
+  // Epilogue through LDS: each wave stages its 64 x 64 outputs (rows m, 128-byte rows, 16-byte chunk c in
+  // slot c ^ (m & 7)) in stage 0, then stores 16 bytes per lane, 8 lanes per row: the 128-byte row pieces
+  // of D are whole cache lines (D's byte strides are multiples of 128 at the reference's shapes).
+  __syncthreads();                               // every wave is done with the stages
+  u8* const stg = st0 + wave * 8192;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
-    const int r = m0 + arow0 + j * 32;
-    if (r >= p.m) continue;
-    u8* drow = p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs;
+    const int m = j * 32 + (lane & 31);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int dn = n0 + wn * (BN / 2) + i * 32 + rr * 8 + (lane >> 5) * 4;
-        const v16f& v = acc[i][j];
-        if (dn + 3 < p.n) {
-          uint2 o;
-          o.x = kg_pack_bf16x2(v[rr * 4 + 0], v[rr * 4 + 1]);
-          o.y = kg_pack_bf16x2(v[rr * 4 + 2], v[rr * 4 + 3]);
-          *reinterpret_cast<uint2*>(drow + 2 * dn) = o;
-        } else {
-#pragma unroll
-          for (int x = 0; x < 4; ++x)
-            if (dn + x < p.n) reinterpret_cast<u16*>(drow)[dn + x] = kg_f32_to_bf16(v[rr * 4 + x]);
-        }
+        const int c = i * 4 + rr;
+        uint2 o;
+        o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+        o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+        *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
       }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): this wave's staging is in LDS
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
+    const uint4 v = *reinterpret_cast<const uint4*>(stg + m * 128 + ((c ^ (m & 7)) << 4));
+    const int r = m0 + wm * (BM / 2) + m, dn = n0 + wn * (BN / 2) + c * 8;
+    if (r < p.m && dn < p.n)
+      *reinterpret_cast<uint4*>(p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs + 2 * dn) = v;
   }
 }
 
 extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
                                long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
                                long long d_hs, void* stream) {
-  KG_CHECK(a && b && d && m >= 0 && m <= rows && n > 0 && n % 4 == 0 && k > 0 && k % 64 == 0 && heads > 0);
-  KG_CHECK(a_rs % 16 == 0 && a_hs % 16 == 0 && b_rs % 16 == 0 && b_hs % 16 == 0 && d_rs % 8 == 0 && d_hs % 8 == 0);
-  KG_CHECK(kg_aligned(a, 16) && kg_aligned(b, 16) && kg_aligned(d, 8));
+  KG_CHECK(a && b && d && m >= 0 && m <= rows && n > 0 && n % 8 == 0 && k > 0 && k % 64 == 0 && heads > 0);
+  KG_CHECK(a_rs % 16 == 0 && a_hs % 16 == 0 && b_rs % 16 == 0 && b_hs % 16 == 0 && d_rs % 16 == 0 &&
+           d_hs % 16 == 0);
+  KG_CHECK(kg_aligned(a, 16) && kg_aligned(b, 16) && kg_aligned(d, 16));
   KG_CHECK(a_rs >= 2ll * k && b_rs >= 2ll * k && 128ll * a_rs < (1ll << 31) && 128ll * b_rs < (1ll << 31));
   if (m == 0) return 0;
   KgBf16Args p{};
