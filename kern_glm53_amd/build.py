@@ -28,7 +28,7 @@ SOURCES = {
     "kg_prep.hip": ["-ffp-contract=off"],
     "kg_fp8_gemm.hip": [],
     "kg_bf16_batched.hip": [],
-    "kg_mqa_logits.hip": [],
+    "kg_mqa_logits.hip": ["-fno-honor-nans"],
 }
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",

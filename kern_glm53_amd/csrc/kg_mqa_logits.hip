@@ -6,12 +6,15 @@
 // rounds only differently in the f32 head summation order.
 //
 // Design: a workgroup of 4 wave64s owns 4 query rows (one per wave, its 32 heads as the rows of the MFMA
-// tiles, kept in registers for the whole key loop) and walks the union of their key ranges 128 keys at a
-// time.  A key block (128 keys x 128 bytes) is copied HBM -> LDS by buffer_load ... lds into one of two
-// LDS stages (XOR-swizzled rows as in the GEMMs) and consumed as 4 key tiles x 2 K halves of
-// v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales).  Each lane of a 32x32 score tile holds one key and 16 of
-// the 32 heads: relu, the head weight (fma) and one cross-half shuffle finish the head sum, then the
-// key scale, and lanes 0-31 store 32 consecutive logits.
+// tiles, kept in registers for the whole key loop) and walks the union of their key ranges 64 keys at a
+// time.  A key block (64 keys x 128 bytes, and the 64 key scales) is copied HBM -> LDS by
+// buffer_load ... lds into one of two LDS stages (XOR-swizzled rows as in the GEMMs) and consumed as
+// 2 key tiles x 2 K halves of v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales).  Each lane of a 32x32
+// score tile holds one key and 16 of the 32 heads: relu and the head weight (fma) give a partial head
+// sum, v_permlane32_swap pairs the two tiles' halves, one add finishes both tiles' sums, then the key
+// scale and one store of 64 consecutive logits.  18 KB of LDS and 122 VGPRs: 4 workgroups per CU.
+// The file is built with -fno-honor-nans, so fmaxf(x, 0) is one v_max_f32: the scores are finite
+// (products of finite e4m3 codes with unit MFMA scales).
 #include "kg_device.h"
 #include "kg_host.h"
 
@@ -33,30 +36,32 @@ KG_DEV v8i kg_lds_frag_m(const u8* p0, const u8* p1) {
   return r;
 }
 
-__global__ __launch_bounds__(256, 2) void kg_mqa_logits_kernel(const u8* __restrict__ q, const u8* __restrict__ kv,
+__global__ __launch_bounds__(256, 4) void kg_mqa_logits_kernel(const u8* __restrict__ q, const u8* __restrict__ kv,
                                                                const float* __restrict__ ksf,
                                                                const float* __restrict__ w,
                                                                const unsigned* __restrict__ ks,
                                                                const unsigned* __restrict__ ke,
                                                                float* __restrict__ logits, int num_q, int num_kv,
                                                                int stride) {
-  // a stage: 128 keys x 128 bytes, then their 128 scales (4 regions of 256 bytes, one per 32-key tile)
-  constexpr int BK = 128, KEYB = BK * 128, STAGE = KEYB + 1024;
+  // a stage: 64 keys x 128 bytes, then 4 regions of 64 key scales (one per wave; region 0 is read)
+  constexpr int BK = 64, TB = BK / 32, KEYB = BK * 128, STAGE = KEYB + 1024;
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
-  __shared__ unsigned srange[2][4];
+  constexpr int NW = 4, NQ = BK / 8 / NW;          // waves (query rows) per workgroup; key DMAs per wave
+  __shared__ unsigned srange[2][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = blockIdx.x * 4 + wave;
+  const int r = blockIdx.x * NW + wave;
   const bool live = r < num_q;
   const unsigned k0 = live ? ks[r] : 0u, k1 = live ? ke[r] : 0u;
   if (lane == 0) srange[0][wave] = live && k1 > k0 ? k0 : 0xffffffffu, srange[1][wave] = live ? k1 : 0u;
   __syncthreads();
-  const unsigned kmin = __builtin_amdgcn_readfirstlane(
-      min(min(srange[0][0], srange[0][1]), min(srange[0][2], srange[0][3])));
-  const unsigned kmax = __builtin_amdgcn_readfirstlane(
-      max(max(srange[1][0], srange[1][1]), max(srange[1][2], srange[1][3])));
+  unsigned kmin = srange[0][0], kmax = srange[1][0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) kmin = min(kmin, srange[0][i]), kmax = max(kmax, srange[1][i]);
+  kmin = __builtin_amdgcn_readfirstlane(kmin);
+  kmax = __builtin_amdgcn_readfirstlane(kmax);
   if (kmin >= kmax) return;                      // uniform: no live key in the workgroup
 
   // query fragments: heads (lane & 31) as MFMA rows, bytes kh*64 + (lane >> 5)*32 .. +32 of the head
@@ -98,76 +103,82 @@ __global__ __launch_bounds__(256, 2) void kg_mqa_logits_kernel(const u8* __restr
   const __amdgpu_buffer_rsrc_t rlg =
       kg_rsrc_m(logits + (size_t)(live ? r : 0) * stride, live ? (long long)stride * 4 : 0);
 
-  // One block's DMA (5 instructions per wave, the count the waits use): 4 x 8 key rows, and the scales of
-  // key tile `wave` (lanes 32.. read past the resource: zeros).
+  // One block's DMA (3 instructions per wave, the count the waits use): 2 x 8 key rows, and the 64 key
+  // scales (every wave reads them, into its own region; region 0 is the one used).
   auto issue = [&](u8* stage, unsigned kb) {
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const unsigned row = kb + (unsigned)(wave * 4 + qq) * 8u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rkv, (KG_LDS void*)(stage + (wave * 4 + qq) * 1024), 16,
+    for (int qq = 0; qq < NQ; ++qq) {
+      const unsigned row = kb + (unsigned)(wave * NQ + qq) * 8u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rkv, (KG_LDS void*)(stage + (wave * NQ + qq) * 1024), 16,
                                                vk[qq & 1] + row * 128u, 0, 0, 0);
     }
-    const unsigned key = kb + (unsigned)wave * 32u + (unsigned)lane;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsf, (KG_LDS void*)(stage + KEYB + wave * 256), 4,
-                                             lane < 32 ? key * 4u : 0x80000000u, 0, 0, 0);
+                                             (kb + (unsigned)lane) * 4u, 0, 0, 0);
   };
-  // MFMAs of key tile t of a stage (two K halves)
+  // the MFMAs of key tile t of a stage (two K halves)
   auto mfma = [&](const u8* stage, v16f& a, int t) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) a[e] = 0.0f;
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      const v8i kf = kg_lds_frag_m(stage + t * 32 * 128 + off[kh][0], stage + t * 32 * 128 + off[kh][1]);
-      a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qf[kh], kf, a, 0, 0, 0, 127, 0, 127);
-    }
+    const v8i k0f = kg_lds_frag_m(stage + t * 32 * 128 + off[0][0], stage + t * 32 * 128 + off[0][1]);
+    const v8i k1f = kg_lds_frag_m(stage + t * 32 * 128 + off[1][0], stage + t * 32 * 128 + off[1][1]);
+    a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qf[0], k0f, v16f{}, 0, 0, 0, 127, 0, 127);
+    a = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(qf[1], k1f, a, 0, 0, 0, 127, 0, 127);
   };
-  // epilogue of key tile t of block kb from its accumulator and key scale: relu, head weights, the
-  // cross-half shuffle, the key scale, one store per wave (always issued: a lane outside [k0, k1) or past
-  // stride gets an offset past the row, which drops it)
-  auto epi = [&](const v16f& a, float sc, unsigned kb, int t) {
-    float s = 0.0f;
+  // relu and head weights of one accumulator: this lane's 16 heads of its key
+  auto hsum = [&](const v16f& a) {
+    float s = wv[0] * fmaxf(a[0], 0.0f);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s = __builtin_fmaf(wv[e], fmaxf(a[e], 0.0f), s);
-    s += __shfl_xor(s, 32, 64);
-    const unsigned key = kb + (unsigned)t * 32u + (unsigned)(lane & 31);
-    const bool ok = lane < 32 && key >= k0 && key < k1 && key - k0 < (unsigned)stride;
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s * sc), rlg, ok ? (key - k0) * 4u : 0x80000000u, 0, 0);
+    for (int e = 1; e < 16; ++e) s = __builtin_fmaf(wv[e], fmaxf(a[e], 0.0f), s);
+    return s;
+  };
+  // Logits of a block's key tiles 0, 1: v_permlane32_swap trades the high half of tile 0's partial sums for
+  // the low half of tile 1's, so one add gives lane l < 32 the sum of tile 0's key l and lane l >= 32 that
+  // of tile 1's key l - 32 (the same low + high order on both), i.e. key kb + l.  Then the key scale and
+  // one store of 64 consecutive logits, always issued: a key outside [ks, ke) or past stride gets an
+  // offset past the row, which drops it.
+  const unsigned lrel = (unsigned)lane - k0;
+  const unsigned lim = live && k1 > k0 ? min(k1 - k0, (unsigned)stride) : 0u;
+  auto store = [&](float x, float y, float sc, unsigned kb) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    const float v = (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * sc;
+    const unsigned rel = kb + lrel;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rlg, rel < lim ? rel * 4u : 0x80000000u, 0, 0);
   };
 
   // Software pipeline over key blocks (two stages, two accumulator sets): the MFMAs of block i + 1 issue
   // between the epilogue steps of block i, so the matrix pipe and the VALU overlap.  Per block:
   //   read block i's key scales (its stage);
-  //   barrier: the DMA of block i + 1 has landed (issued after it: the previous block's 4 logits stores,
-  //            none before the first block) and every wave is done reading block i's stage;
+  //   barrier: the DMA of block i + 1 has landed (issued before the previous block's logits store; nothing
+  //            is stored before the first block) and every wave is done reading block i's stage;
   //   DMA of block i + 2 into block i's stage; MFMAs of block i + 1 interleaved with block i's epilogue.
-  v16f acc0[4], acc1[4];
+  // The last block's MFMAs of the following stage run on whatever it holds and are discarded.
+  v16f acc0[TB], acc1[TB];
   issue(st0, kmin);
   issue(st1, kmin + BK);                         // (past kmax or num_kv: read, never stored)
-  asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
+  static_assert(NQ == 2 && TB == 2, "the waits count 3 DMA instructions and 1 store per block");
 #pragma unroll
-  for (int t = 0; t < 4; ++t) mfma(st0, acc0[t], t);
+  for (int t = 0; t < TB; ++t) mfma(st0, acc0[t], t);
 
-  // (a plain block, not do-while: its `break` leaves the key loop)
-#define KG_MQA_BLOCK(CUR, NXT, AC, AN)                                                                      \
-  {                                                                                                       \
-    const bool more_ = kb + BK < kmax;                                                                     \
-    float sc_[4];                                                                                         \
-    _Pragma("unroll") for (int t = 0; t < 4; ++t)                                                          \
-      sc_[t] = *reinterpret_cast<const float*>((CUR) + KEYB + t * 256 + (lane & 31) * 4);                 \
-    if (kb == kmin) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");              \
-    else asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");                         \
+#define KG_MQA_BLOCK(CUR, NXT, AC, AN, VMCNT)                                                               \
+  do {                                                                                                    \
+    const float sc_ = *reinterpret_cast<const float*>((CUR) + KEYB + lane * 4);                           \
+    asm volatile("s_waitcnt vmcnt(" VMCNT ") lgkmcnt(0)\n\ts_barrier" ::: "memory");                      \
     issue(CUR, kb + 2 * BK);                                                                              \
-    _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                                        \
-      if (more_) mfma(NXT, AN[t], t);                                                                     \
-      epi(AC[t], sc_[t], kb, t);                                                                          \
-    }                                                                                                     \
-    if (!more_) break;                                                                                    \
+    __builtin_amdgcn_sched_barrier(0);             /* the DMA goes out first */                           \
+    mfma(NXT, AN[0], 0);                                                                                  \
+    const float h0_ = hsum(AC[0]);                                                                        \
+    mfma(NXT, AN[1], 1);                                                                                  \
+    const float h1_ = hsum(AC[1]);                                                                        \
+    store(h0_, h1_, sc_, kb);                                                                             \
     kb += BK;                                                                                             \
-  }
+  } while (0)
+  // Blocks go in pairs with one exit test per pair, so that each block is one basic block and its MFMAs
+  // stay between its epilogue steps; a pair's second block may lie past kmax: its keys are past every
+  // row's ke, so its store drops.
   unsigned kb = kmin;
-  for (;;) {
-    KG_MQA_BLOCK(st0, st1, acc0, acc1);          // block kb: stage 0, acc0
-    KG_MQA_BLOCK(st1, st0, acc1, acc0);          // block kb: stage 1, acc1
+  KG_MQA_BLOCK(st0, st1, acc0, acc1, "0");       // the first block: nothing stored yet
+  while (kb < kmax) {
+    KG_MQA_BLOCK(st1, st0, acc1, acc0, "1");
+    KG_MQA_BLOCK(st0, st1, acc0, acc1, "1");
   }
 #undef KG_MQA_BLOCK
   __builtin_amdgcn_s_waitcnt(0);                 // no DMA into LDS may be in flight at exit

@@ -264,6 +264,18 @@ def test_mqa_logits_ragged():
     check_mqa(out, q8, k8, ksf, w, ks, ke, stride)
 
 
+@pytest.mark.parametrize("num_kv", [50, 64, 65, 129])
+def test_mqa_logits_short(num_kv):
+    """Key ranges of one or two 64-key blocks (the loop runs blocks in pairs: the extra block stores nothing)."""
+    num_q, stride = 6, 160
+    q8, k8, ksf, w = mqa_case(num_q, num_kv, 55 + num_kv)
+    rng = np.random.default_rng(num_kv)
+    ks = rng.integers(0, num_kv, num_q)
+    ke = np.minimum(ks + rng.integers(1, num_kv + 1, num_q), num_kv)
+    out = run_mqa(q8, k8, ksf, w, ks, ke, stride)
+    check_mqa(out, q8, k8, ksf, w, ks, ke, stride)
+
+
 def test_mqa_logits_causal_chunk():
     """The benchmark's shape at reduced size: the last 256 rows of one 4096-token sequence, causal."""
     num_q, num_kv, stride = 256, 4096, 4096
