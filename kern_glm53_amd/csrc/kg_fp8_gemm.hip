@@ -395,21 +395,23 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 // ---------------------------------------------------------------- persistent 256 x 256 kernel
 //
 // One workgroup per CU walks output tiles (round r: tile r * gridDim.x + its slot, each full round spread
-// over the XCDs in contiguous chunks).  K advances in sub-steps of 64 through a ring of four LDS stages of
-// 32 KB (256 A rows + 256 W rows of 64 bytes), each its own __shared__ array.  The DMA of sub-step s + 4
-// is issued right after the barrier of sub-step s, so a copy has three sub-steps (48 MFMAs per wave) to
-// land, and the ring runs on across tiles: the next tile's first four sub-steps and its first scale words
-// are in flight while this tile's epilogue runs.
+// over the XCDs in contiguous chunks).  K advances in stages of 128 (one scale block) through two LDS
+// buffers of 64 KB (256 A rows + 256 W rows of 128 bytes), each its own __shared__ array.  128-byte rows
+// make every DMA lane group of 8 read one whole 128-byte line: half as many L2 requests as 64-byte rows,
+// which is what bounds the vector-memory path here.  One barrier per stage, after the stage's last read
+// of its own buffer: it publishes the next stage (whose DMA this wave waited for) and frees this stage's
+// buffer, into which the DMA of the stage after next then goes.  The ring runs on across tiles: the next
+// tile's first stages and its first scale words are in flight while this tile's epilogue runs.
 //
-// LDS rows are 64 bytes; 16-byte chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 rows of a
-// ds_read_b128 phase cover the 64 banks once and a DMA instruction (16 rows, lanes row-major) needs one
-// lane offset.
+// LDS rows are 128 bytes; 16-byte chunk c of row r sits in slot c ^ ((r >> 1) & 7), so the 16 rows of a
+// ds_read_b128 phase cover the 64 banks once.  A DMA instruction covers 8 rows (lane l: row l >> 3, slot
+// l & 7) starting at a multiple of 8, so its lanes' chunk depends on the instruction's parity only.
 //
 // Bounds: a buffer load's range check covers its VGPR offset only, so every row offset goes into the VGPR
 // offset and only the K offset into the scalar one (it stays inside the row).  A rows past the tile are
 // the next rows of the buffer or zeros past it; W rows past n read zeros; their outputs are not stored.
-// K per tile is padded to a multiple of 512 (eight sub-steps): a padded sub-step reads zeros (null
-// resource) with unit scales.
+// K per tile is padded to a multiple of 512 (four stages): a padded stage reads zeros (null resource)
+// with unit scales.
 
 struct KgPTile {                      // one tile (wave-uniform)
   int m0, m_end, nt, g;
@@ -470,19 +472,19 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 
 // Epilogue of the persistent kernel for modes 0 and 1: bf16 through LDS, so that each store writes 16
 // contiguous bytes per lane and 16 lanes cover a 256-byte row segment.  Per m tile j (32 rows), each wave
-// stages its 32 x 128 outputs (8 KB) in the ring stage that is idle during the epilogue, split into the
-// two 4 KB pieces this wave's own DMA writes (so no other wave's DMA into that stage can overlap them).
+// stages its 32 x 128 outputs (8 KB) in `stage`: the 64 weight rows of the last stage's buffer that only
+// this wave's DMA writes, and not before the next tile's first stage (so no other wave touches them).
 // Rows are 256 bytes; chunk c (8 columns) of row m sits in slot c ^ (m & 15), with its two 8-byte halves
 // swapped when m & 16, which makes the 8-byte writes of a wave's 32 rows conflict-free.
-KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int wave, int m0, int m_end,
+KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int m0, int m_end,
                                 int n0, int wm, int wn, bool half) {
   // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
   // tile, rather than hoisted out of the tile loop into registers the K loop needs.
   int lane;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
   const __amdgpu_buffer_rsrc_t rc = kg_rsrc(p.c, (long long)p.rows * p.ldc * 2);
-  u8* const lo = stage + wave * 4096;            // rows 0..15 of the wave's staging
-  u8* const hi = stage + 256 * 64 + wave * 4096;  // rows 16..31
+  u8* const lo = stage;                          // rows 0..15 of the wave's staging
+  u8* const hi = stage + 4096;                   // rows 16..31
   const int mr = lane & 31;                       // this lane's row when writing
   u8* const wrow = (mr < 16 ? lo : hi) + (mr & 15) * 256;
   const int hsel = (lane >> 5) ^ ((lane >> 4) & 1);
@@ -514,8 +516,8 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
         v.x = v.z, v.y = v.w, v.z = x, v.w = y;
       }
       const int gm = rbase + j * 32 + m, gn = n0 + wn * 128 + c * 8;
-      // always issued (a fixed count of 32 stores per wave and tile, which the K loop's waits count on);
-      // lanes outside the tile's rows or columns get an offset past the resource, which drops the write
+      // always issued (no branch); lanes outside the tile's rows or columns get an offset past the
+      // resource, which drops the write
       const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
       __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
       __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
@@ -529,10 +531,10 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
 // pair with its up accumulators i + 2 at the same output columns.  Same arithmetic as the unfused pair
 // (bf16 gate_up output, then glm_silu_mul_quant): g and u are rounded to bf16, v = bf16(silu(g) u), the
 // 128-column amax goes through LDS (xam) to the wave holding the other 64 columns of the row.  The e4m3
-// codes of the whole 256 x 128 output tile are staged in LDS (the idle ring stage, row r at r * 128 with
-// 16-byte chunk c in slot c ^ (r & 7)) and then stored a full 128-byte row segment per 8 lanes: every
-// wave issues exactly 8 code stores and 1 exponent-byte store (offsets past the resource drop the rows
-// past the tile), a count the next tile's first barriers wait on.
+// codes of the whole 256 x 128 output tile are staged in LDS (the weight half of the last stage's
+// buffer, which no DMA writes before the next tile's first stage: row r at r * 128 with 16-byte chunk c
+// in slot c ^ (r & 7)) and then stored a full 128-byte row segment per 8 lanes: every wave issues 8 code
+// stores and 1 exponent-byte store (offsets past the resource drop the rows past the tile).
 KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, float (*xam)[256], u8* xe,
                                  int wave, int m0, int m_end, int nt, int wm, int wn, bool half) {
   int lane;   // from a volatile read: keeps the per-lane address math here rather than hoisted
@@ -592,7 +594,7 @@ KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stag
     const unsigned off = gm < m_end ? (unsigned)((((nt >> 2) * p.sf_rows + gm) << 2) + (nt & 3)) : 0x80000000u;
     __builtin_amdgcn_raw_buffer_store_b8((u8)xe[r], rs, off, 0, 0);
   }
-  // staging reads done in every wave before the ring's next DMA into the stage; the stores stay in flight
+  // staging reads done in every wave before the ring's next DMA into these rows; the stores stay in flight
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -605,14 +607,10 @@ KG_DEV int kg_round_tile(int r, int live) {
 
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args p) {
-  constexpr int BM = 256, BN = 256, TI = 4, TJ = 4, NO = 4, NI = 4, SA = 256 * 64, STAGE = 512 * 64;
-  constexpr int BAR = (NO - 2) * NI + 1;      // MFMA slot after which a sub-step's barrier sits
-  constexpr int NSLOT = NO * NI - 1 - BAR;    // slots after it
+  constexpr int BM = 256, BN = 256, TI = 4, TJ = 4, NO = 4, NI = 4, NIH = 2, SA = 256 * 128, STAGE = 512 * 128;
   constexpr int CN = MODE == 2 ? 128 : 256;   // output columns (of n) per column tile
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
-  __shared__ __attribute__((aligned(1024))) u8 st2[STAGE];
-  __shared__ __attribute__((aligned(1024))) u8 st3[STAGE];
   __shared__ int ps[MODE == 0 ? 1 : 1024], tp[MODE == 0 ? 1 : 1024], wtot[4];
   __shared__ float xam[MODE == 2 ? 2 : 1][BM];
   __shared__ u8 xe[MODE == 2 ? BM : 1];
@@ -668,53 +666,65 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   const int idx = kg_round_tile(round, live);
   if (idx < 0) return;                         // uniform
 
-  const int KS = ((p.k + 511) >> 9) << 3;      // sub-steps per tile (padded to a multiple of 8)
+  const int KS = ((p.k + 511) >> 9) << 2;      // stages per tile (padded to a multiple of 4)
   const int KB = p.k >> 7;                     // live K blocks of 128
   const int half = p.n >> 1, kw = (p.k + 511) >> 9;
   const __amdgpu_buffer_rsrc_t rnull = kg_rsrc(p.a, 0);
   const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a, (long long)p.rows * p.lda);
   const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
 
-  // per-lane DMA offsets: instruction q of this wave covers rows 16 (4 wave + q) .. + 15 of the tile
-  const int dchunk = ((lane & 3) ^ ((lane >> 4) & 3)) << 4;
-  unsigned va[4], vw[4];
+  // Per-lane DMA offsets: instruction q (0..7) of this wave covers tile rows 8 (8 wave + q) .. + 7, lane l
+  // row + (l >> 3) and the chunk that belongs in LDS slot l & 7: (l & 7) ^ (4 (q & 1) + (l >> 4)).
+  unsigned va[2], vw[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = (wave * 4 + q) * 16 + (lane >> 2);
-    va[q] = (unsigned)(r * p.lda + dchunk);
-    vw[q] = (unsigned)(kg_wrow<MODE, 256>(0, half, r) * p.k + dchunk);
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = ((lane & 7) ^ ((par << 2) | (lane >> 4))) << 4;
+    va[par] = (unsigned)((lane >> 3) * p.lda + chunk);
+    vw[par] = (unsigned)((lane >> 3) * p.k + chunk);
   }
-  // per-lane fragment offsets (every fragment row is (lane & 31) plus a multiple of 32)
+  // per-lane fragment offsets [K half][16-byte half]; every fragment row is (lane & 31) plus a multiple of
+  // 32, so ((row >> 1) & 7) is the same for all of them
   const int arow0 = wm * (BM / 2) + (lane & 31);
   const int wbase = MODE == 2 ? wn * (BN / 4) : wn * (BN / 2);
   auto wtile = [](int i) -> int {
     if constexpr (MODE == 2) return i < TI / 2 ? i * 32 : BN / 2 + (i - TI / 2) * 32;
     else return i * 32;
   };
-  unsigned offa[2], offw[2];
+  unsigned offa[2][2], offw[2][2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const unsigned sw = (unsigned)((((lane >> 5) * 2 + h) ^ (((lane & 31) >> 2) & 3)) << 4);
-    offa[h] = (unsigned)arow0 * 64u + sw;
-    offw[h] = (unsigned)SA + (unsigned)(wbase + (lane & 31)) * 64u + sw;
-  }
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned sw = (unsigned)(((kh * 4 + (lane >> 5) * 2 + h) ^ (((lane & 31) >> 1) & 7)) << 4);
+      offa[kh][h] = (unsigned)arow0 * 128u + sw;
+      offw[kh][h] = (unsigned)SA + (unsigned)(wbase + (lane & 31)) * 128u + sw;
+    }
 
   auto dsrc = [&](const KgPTile& t) { return kg_dma_src(p, t, CN); };
-  // DMA instruction q (0..3: A rows 16 (4 wave + q) .., 4..7: the same W rows) of the sub-step at K offset
-  // ko into stage st; past K, or with no tile, it reads zeros
+  // DMA instruction q of a stage (0..7: A rows 8 (8 wave + q) .., 8..15: the same W rows) at K offset ko
+  // into buffer st; past K, or with no tile, it reads zeros.  A half tile's rows 128.. are read as zeros
+  // (never used).  Instructions 0..3 go out after the barrier of the stage before, 4..15 during the stage
+  // after it: the weight rows of a buffer stay untouched until the next stage begins.
+  // The per-instruction row and LDS offsets are formed at each instruction from laundered per-wave bases:
+  // kept as 16 precomputed values per buffer, they would not fit in registers (spills, whose reloads wait
+  // for the whole DMA queue).
+  const unsigned arow_w = (unsigned)(wave * 64) * (unsigned)p.lda;
+  const unsigned wrow_w = (unsigned)kg_wrow<MODE, 256>(0, half, wave * 64) * (unsigned)p.k;
   auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
     const bool in = ko < p.k && d.ok;
-    if (q < 4)   // (a half tile's rows 128.. read zeros; the instruction is issued all the same)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(in && !(d.half && wave >= 2) ? ra : rnull,
-                                               (KG_LDS void*)(st + (wave * 4 + q) * 1024), 16, va[q] + d.abase, ko,
-                                               0, 0);
-    else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(in ? d.rw : rnull, (KG_LDS void*)(st + SA + (wave * 4 + q - 4) * 1024),
-                                               16, vw[q - 4] + d.wbase, ko, 0, 0);
+    const int j = q & 7;
+    unsigned v = q < 8 ? va[j & 1] : vw[j & 1];
+    unsigned u = q < 8 ? arow_w + d.abase : wrow_w + d.wbase;
+    unsigned l = (unsigned)(wave * 8192);
+    asm volatile("" : "+v"(v));
+    v += u + (unsigned)(j * 8) * (unsigned)(q < 8 ? p.lda : p.k);
+    const __amdgpu_buffer_rsrc_t rs = q < 8 ? (in && !(d.half && wave >= 2) ? ra : rnull) : (in ? d.rw : rnull);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KG_LDS void*)(st + (q < 8 ? 0 : SA) + l + j * 1024), 16, v, ko, 0,
+                                             0);
   };
   // Scale words of word row kg4 (the exponent bytes of K blocks 4 kg4 .. 4 kg4 + 3, byte kb & 3) of tile t;
-  // the MFMA picks its byte with op_sel.  wa/wb[0] is the word group in use, [1] the next one, loaded four
-  // sub-steps before it is needed.
+  // the MFMA picks its byte with op_sel.  wa/wb[0] is the word group in use, [1] the next one, loaded two
+  // stages before it is needed.
   u32 wa[2][TJ], wb[2][TI];
   auto words = [&](const KgPTile& t, int kg4, u32* xa, u32* xb) {
     const __amdgpu_buffer_rsrc_t rsb =
@@ -733,8 +743,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   v16f acc[TI][TJ];
   v8i res[2][NI], str[2];
 
-#define KG_PFRAG_W(ST, I) kg_lds_frag((ST) + wtile(I) * 64, offw[0], offw[1])
-#define KG_PFRAG_A(ST, J) kg_lds_frag((ST) + (J) * 2048, offa[0], offa[1])
+#define KG_PFRAG_W(ST, KH, I) kg_lds_frag((ST) + wtile(I) * 128, offw[KH][0], offw[KH][1])
+#define KG_PFRAG_A(ST, KH, J) kg_lds_frag((ST) + (J) * 4096, offa[KH][0], offa[KH][1])
+#define KG_PFRAG_AH(ST, KH, J) kg_lds_frag((ST) + (J) * 4096 - wm * 8192, offa[KH][0], offa[KH][1])
   // The waits count on the issue order of the DMA and word loads: neither the IR passes nor the scheduler
   // may swap them.
 #define KG_ISSUE_ORDER()                                                                                   \
@@ -742,95 +753,91 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     asm volatile("" ::: "memory");                                                                        \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
   } while (0)
-  // One sub-step s (PH = its index in the group of eight; K block PH / 2 of the word group): 16 MFMAs of
-  // K 64 from stage CUR.  Every other MFMA slot issues one DMA instruction of sub-step s + 3 into PRV, the
-  // stage of sub-step s - 1, which every wave finished reading before the previous barrier; spreading the
-  // eight instructions keeps the vector-memory queue from stalling the MFMA issue.  The barrier after
-  // slot BAR waits for this wave's DMA of sub-step s + 1 and publishes it; the slots after it read NXT's
-  // first fragments.  PH 4 first issues the next word group's 8 loads.  After an epilogue its stores
-  // (32 in modes 0/1, 9 in mode 2, issued after the DMA of the tile's sub-steps 1 and 2) are still in
-  // flight at the barriers of the tile's sub-steps 0 and 1, which then count 45 (22).  Loads issued after the DMA of
-  // s + 1 (the last of sub-step s - 2) when the barrier waits: sub-step s - 1's 8, this sub-step's 5 up to
-  // slot BAR, and the 8 words if PH 4 is s - 1 or s: 21 on PH 4, 5, else 13.  The last group's sub-steps
-  // 5..7 load the next tile's first three (dsn), as its PH 4 loads the next tile's first word group.
-#define KG_PSUB(CUR, NXT, PRV, PH)                                                                         \
+  // One stage s (PH = its index in the group of four = the byte of the scale words): 2 K halves x 16
+  // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  Slots 0..11 issue DMA
+  // instructions 4..15 of stage s + 1 into OTH (D1 / K1), one per MFMA; slots 1..4 read the second K
+  // half's A fragments; the W fragment of row o + 1 is read at (o, n = 0), the second half's row 0 at
+  // slot 12, so the last read of CUR is at slot 24.  The barrier after slot 25 waits for this wave's DMA
+  // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 12 after it),
+  // publishes it and frees CUR: slots 26..29 issue instructions 0..3 of stage s + 2 into CUR (D2 / K2),
+  // slots 26..30 read stage s + 1's first fragments from OTH.
+#define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2)                                                            \
   do {                                                                                                    \
-    if constexpr ((PH) == 4) {                                                                             \
-      words(wt, wkg, wa[1], wb[1]);                                                                        \
-      KG_ISSUE_ORDER();                                                                                   \
-    }                                                                                                     \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
-    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
-      _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                     \
-        acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[(PH) & 1][n], acc[o][n], \
-                                                                    0, 0, (PH) >> 1, (int)wb[0][o],       \
-                                                                    (PH) >> 1, (int)wa[0][n]);            \
-        const int slot_ = o * NI + n;                                                                      \
-        if (slot_ % 2 == 0) {                                                                             \
-          if constexpr ((PH) < 5) dma1(PRV, dsc, (ks + (PH) + 3) * 64, slot_ / 2);                          \
-          else dma1(PRV, dsn, dko + ((PH) - 5) * 64, slot_ / 2);                                           \
-        }                                                                                                 \
-        if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, o + 1);                               \
-        if (slot_ == BAR) {                                                                               \
-          if constexpr ((PH) == 4 || (PH) == 5)                                                            \
-            asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else if ((PH) <= 1 && ks == 0 && stores_pending && MODE == 2)                                    \
-            asm volatile("s_waitcnt vmcnt(22) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else if ((PH) <= 1 && ks == 0 && stores_pending)                                                 \
-            asm volatile("s_waitcnt vmcnt(45) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else                                                                                            \
-            asm volatile("s_waitcnt vmcnt(13) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-        } else if (slot_ > BAR) {                                                                         \
-          _Pragma("unroll") for (int u = 0; u < NI + 1; ++u) {                                             \
-            if (u * NSLOT / (NI + 1) != slot_ - BAR - 1) continue;                                         \
-            if (u < NI) res[((PH) + 1) & 1][u] = KG_PFRAG_A(NXT, u);                                       \
-            else str[0] = KG_PFRAG_W(NXT, 0);                                                              \
+    _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
+      _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                     \
+        _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                   \
+          const int t_ = kh * 16 + o * NI + n;                                                             \
+          acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
+                                                                      (PH), (int)wb[0][o], (PH),          \
+                                                                      (int)wa[0][n]);                     \
+          if (t_ < 12) dma1(OTH, D1, K1, 4 + t_);                                                          \
+          if (t_ == 12 && (PH) == 2) {                                                                     \
+            KG_ISSUE_ORDER();                                                                             \
+            words(wt, wkg, wa[1], wb[1]);                                                                 \
+            KG_ISSUE_ORDER();                                                                             \
           }                                                                                               \
+          if (kh == 0 && t_ >= 1 && t_ <= 4) res[1][t_ - 1] = KG_PFRAG_A(CUR, 1, t_ - 1);                  \
+          if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
+          if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
+          if (t_ == 25) {                                                                                 \
+            if constexpr ((PH) == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); \
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                 \
+          }                                                                                               \
+          if (t_ >= 26 && t_ <= 29) dma1(CUR, D2, K2, t_ - 26);                                            \
+          if (t_ == 26) res[0][0] = KG_PFRAG_A(OTH, 0, 0);                                                 \
+          if (t_ == 27) res[0][1] = KG_PFRAG_A(OTH, 0, 1);                                                 \
+          if (t_ == 28) str[0] = KG_PFRAG_W(OTH, 0, 0);                                                    \
+          if (t_ == 29) res[0][2] = KG_PFRAG_A(OTH, 0, 2);                                                 \
+          if (t_ == 30) res[0][3] = KG_PFRAG_A(OTH, 0, 3);                                                 \
+          __builtin_amdgcn_sched_barrier(0);                                                              \
         }                                                                                                 \
-        __builtin_amdgcn_sched_barrier(0);                                                                \
       }                                                                                                   \
     }                                                                                                     \
   } while (0)
 
   // Half tiles (at most 128 rows, an expert's tail): the 4 waves split 2 x 2 over 128 x 256, so a wave
-  // owns rows wm * 64 + 32 j (j < 2) against the same 128 weight rows: 8 MFMAs per sub-step.  The DMA is
-  // the same 8 instructions per sub-step (waves 2, 3 load zeros for A), one per MFMA slot; the barrier
-  // after slot BARH = 5 counts this sub-step's 6, so 14 (22 on PH 4, 5; 46 / 23 after an epilogue).
-  constexpr int NIH = 2, BARH = (NO - 2) * NIH + 1, NSLOTH = NO * NIH - 1 - BARH;
-#define KG_PFRAG_AH(ST, J) kg_lds_frag((ST) + (J) * 2048 - wm * 4096, offa[0], offa[1])
-#define KG_PSUBH(CUR, NXT, PRV, PH)                                                                        \
+  // owns rows wm * 64 + 32 j (j < 2) against the same 128 weight rows: 2 x 8 MFMAs per stage, slot
+  // t = 8 kh + 2 o + n.  The same 16 DMA instructions per stage, two per slot: 4..15 of stage s + 1 in
+  // slots 0..5, 0..3 of stage s + 2 in slots 14, 15; the last read of CUR is at slot 12, the barrier
+  // after slot 13; the words go out at slot 6 of PH 2.
+#define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2)                                                           \
   do {                                                                                                    \
-    if constexpr ((PH) == 4) {                                                                             \
-      words(wt, wkg, wa[1], wb[1]);                                                                        \
-      KG_ISSUE_ORDER();                                                                                   \
-    }                                                                                                     \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
-    _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
-      _Pragma("unroll") for (int n = 0; n < NIH; ++n) {                                                    \
-        acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[(PH) & 1][n], acc[o][n], \
-                                                                    0, 0, (PH) >> 1, (int)wb[0][o],       \
-                                                                    (PH) >> 1, (int)wa[0][n]);            \
-        const int slot_ = o * NIH + n;                                                                     \
-        if constexpr ((PH) < 5) dma1(PRV, dsc, (ks + (PH) + 3) * 64, slot_);                                \
-        else dma1(PRV, dsn, dko + ((PH) - 5) * 64, slot_);                                                 \
-        if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, o + 1);                               \
-        if (slot_ == BARH) {                                                                              \
-          if constexpr ((PH) == 4 || (PH) == 5)                                                            \
-            asm volatile("s_waitcnt vmcnt(22) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else if ((PH) <= 1 && ks == 0 && stores_pending && MODE == 2)                                    \
-            asm volatile("s_waitcnt vmcnt(23) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else if ((PH) <= 1 && ks == 0 && stores_pending)                                                 \
-            asm volatile("s_waitcnt vmcnt(46) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-          else                                                                                            \
-            asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");                     \
-        } else if (slot_ > BARH) {                                                                        \
-          _Pragma("unroll") for (int u = 0; u < NIH + 1; ++u) {                                            \
-            if (u * NSLOTH / (NIH + 1) != slot_ - BARH - 1) continue;                                      \
-            if (u < NIH) res[((PH) + 1) & 1][u] = KG_PFRAG_AH(NXT, u);                                     \
-            else str[0] = KG_PFRAG_W(NXT, 0);                                                              \
+    _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
+      _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                     \
+        _Pragma("unroll") for (int n = 0; n < NIH; ++n) {                                                  \
+          const int t_ = kh * 8 + o * NIH + n;                                                             \
+          acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
+                                                                      (PH), (int)wb[0][o], (PH),          \
+                                                                      (int)wa[0][n]);                     \
+          if (t_ < 6) {                                                                                   \
+            dma1(OTH, D1, K1, 4 + 2 * t_);                                                                \
+            dma1(OTH, D1, K1, 5 + 2 * t_);                                                                \
           }                                                                                               \
+          if (t_ == 6 && (PH) == 2) {                                                                      \
+            KG_ISSUE_ORDER();                                                                             \
+            words(wt, wkg, wa[1], wb[1]);                                                                 \
+            KG_ISSUE_ORDER();                                                                             \
+          }                                                                                               \
+          if (kh == 0 && t_ >= 1 && t_ <= 2) res[1][t_ - 1] = KG_PFRAG_AH(CUR, 1, t_ - 1);                 \
+          if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
+          if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
+          if (t_ == 13) {                                                                                 \
+            if constexpr ((PH) == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); \
+            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                 \
+          }                                                                                               \
+          if (t_ >= 14) {                                                                                 \
+            dma1(CUR, D2, K2, 2 * (t_ - 14));                                                             \
+            dma1(CUR, D2, K2, 2 * (t_ - 14) + 1);                                                         \
+          }                                                                                               \
+          if (t_ == 14) {                                                                                 \
+            res[0][0] = KG_PFRAG_AH(OTH, 0, 0);                                                           \
+            str[0] = KG_PFRAG_W(OTH, 0, 0);                                                               \
+          }                                                                                               \
+          if (t_ == 15) res[0][1] = KG_PFRAG_AH(OTH, 0, 1);                                                \
+          __builtin_amdgcn_sched_barrier(0);                                                              \
         }                                                                                                 \
-        __builtin_amdgcn_sched_barrier(0);                                                                \
       }                                                                                                   \
     }                                                                                                     \
   } while (0)
@@ -842,32 +849,29 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   nxt.g = -1;
   if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
 
-  // ---- prologue: the first word group, then sub-steps 0..2 of the first tile in flight (sub-step 0's
-  // slots issue sub-step 3, as in the ring), then sub-step 0's fragments
-  KgDmaSrc dsc = dsrc(cur), dsn = dsrc(nxt);
+  // ---- prologue: the first word group, stage 0 and instructions 0..3 of stage 1 (as the ring has them
+  // at a stage's start)
+  KgDmaSrc dsc = dsrc(cur);
   words(cur, 0, wa[0], wb[0]);
   KG_ISSUE_ORDER();
 #pragma unroll
-  for (int d = 0; d < 3; ++d) {
-    u8* const st = d == 0 ? st0 : d == 1 ? st1 : st2;
+  for (int q = 0; q < 16; ++q) dma1(st0, dsc, 0, q);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) dma1(st, dsc, d * 64, q);
-    KG_ISSUE_ORDER();
-  }
-  asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  for (int q = 0; q < 4; ++q) dma1(st1, dsc, 128, q);
+  KG_ISSUE_ORDER();
+  asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
 
-  bool stores_pending = false;
   for (;;) {
     const bool halft = cur.m_end - cur.m0 <= 128;
-    // sub-step 0's first fragments (stage 0 holds the tile's sub-step 0, published by the last barrier;
-    // read here because the previous tile may have had the other shape)
-    str[0] = KG_PFRAG_W(st0, 0);
+    // stage 0's first fragments (buffer 0 holds the tile's stage 0, published by the last barrier; read
+    // here because the previous tile may have had the other shape)
+    str[0] = KG_PFRAG_W(st0, 0, 0);
     if (halft) {
 #pragma unroll
-      for (int n = 0; n < NIH; ++n) res[0][n] = KG_PFRAG_AH(st0, n);
+      for (int n = 0; n < NIH; ++n) res[0][n] = KG_PFRAG_AH(st0, 0, n);
     } else {
 #pragma unroll
-      for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, n);
+      for (int n = 0; n < NI; ++n) res[0][n] = KG_PFRAG_A(st0, 0, n);
     }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -875,61 +879,51 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    // per group of eight sub-steps: blocks of the word group at or past K (K % 512 != 0) get the unit
-    // exponent 127; the last group hands the ring over to the next tile (its first word group on PH 4, its
-    // first three sub-steps on PH 5..7)
+    // Per group of four stages: blocks of the word group at or past K (K % 512 != 0) get the unit
+    // exponent 127; the DMA of the next group's stages 0, 1 (issued from stages 2, 3) comes from the next
+    // tile in the last group (dsn, K 0), as do the words loaded on PH 2.
 #define KG_GROUP_START()                                                                                   \
-  const int live_b = KB - (ks >> 1);                                                                        \
+  const int live_b = KB - ks;                                                                              \
   if (live_b < 4) {                                                                                        \
     const u32 keep = live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));                               \
     _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | (0x7f7f7f7fu & ~keep);   \
     _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | (0x7f7f7f7fu & ~keep);   \
   }                                                                                                        \
-  const bool lastg = ks + 8 >= KS;                                                                         \
+  const bool lastg = ks + 4 >= KS;                                                                         \
   const KgPTile wt = lastg ? nxt : cur;                                                                    \
-  const int dko = lastg ? 0 : (ks + 8) * 64, wkg = lastg ? 0 : (ks >> 3) + 1;                              \
-  dsn = dsrc(wt)
+  const int kn = lastg ? 0 : (ks + 4) * 128, wkg = lastg ? 0 : (ks >> 2) + 1;                              \
+  const KgDmaSrc dsn = dsrc(wt);                                                                           \
+  const int k0 = ks * 128
 #define KG_GROUP_END()                                                                                     \
   _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
   _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i]
     if (halft) {
-      for (int ks = 0; ks < KS; ks += 8) {
+      for (int ks = 0; ks < KS; ks += 4) {
         KG_GROUP_START();
-        KG_PSUBH(st0, st1, st3, 0);
-        KG_PSUBH(st1, st2, st0, 1);
-        KG_PSUBH(st2, st3, st1, 2);
-        KG_PSUBH(st3, st0, st2, 3);
-        KG_PSUBH(st0, st1, st3, 4);
-        KG_PSUBH(st1, st2, st0, 5);
-        KG_PSUBH(st2, st3, st1, 6);
-        KG_PSUBH(st3, st0, st2, 7);
+        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
     } else {
-      for (int ks = 0; ks < KS; ks += 8) {
+      for (int ks = 0; ks < KS; ks += 4) {
         KG_GROUP_START();
-        KG_PSUB(st0, st1, st3, 0);
-        KG_PSUB(st1, st2, st0, 1);
-        KG_PSUB(st2, st3, st1, 2);
-        KG_PSUB(st3, st0, st2, 3);
-        KG_PSUB(st0, st1, st3, 4);
-        KG_PSUB(st1, st2, st0, 5);
-        KG_PSUB(st2, st3, st1, 6);
-        KG_PSUB(st3, st0, st2, 7);
+        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
     }
 #undef KG_GROUP_START
 #undef KG_GROUP_END
     kg_mfma_drain();
-    // stage 3 is idle until the next tile's first sub-step issues its DMA
+    // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
     if constexpr (MODE == 2)
-      kg_fp8_epilogue_silu(p, acc, st3, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
+      kg_fp8_epilogue_silu(p, acc, st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
     else
-      kg_fp8_epilogue_lds(p, acc, st3, wave, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
-    // the epilogue's stores (32, or 9 in mode 2, per wave) stay in flight, counted by the next tile's
-    // first two barriers
-    stores_pending = true;
+      kg_fp8_epilogue_lds(p, acc, st1 + SA + wave * 8192, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
     if (nidx < 0) break;
     ++round;
     cur = nxt;
@@ -939,8 +933,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
   }
   __builtin_amdgcn_s_waitcnt(0);
-#undef KG_PSUB
-#undef KG_PSUBH
+#undef KG_PSTAGE
+#undef KG_PSTAGEH
 #undef KG_PFRAG_AH
 #undef KG_ISSUE_ORDER
 #undef KG_PFRAG_A
