@@ -5,11 +5,14 @@
 // HBM-bound (102-169 flop/B against a bf16 ridge of ~315): the design goal is streaming A and D once at
 // full width while the MFMA work hides under it.
 //   * a workgroup = 4 wave64s owns a 128-row x 128-column tile of one head; K advances 64 (128 bytes of a
-//     row) per stage through LDS, copied HBM -> LDS by buffer_load ... lds with the same XOR-swizzled
-//     128-byte rows as the fp8 GEMM; two stages in two distinct LDS arrays;
+//     row) per stage through one 32 KB LDS stage, copied HBM -> LDS by buffer_load ... lds with the same
+//     XOR-swizzled 128-byte rows as the fp8 GEMM.  K is short here (192 or 512): four workgroups per CU
+//     (100 VGPRs, 32 KB of LDS each) overlap each other's copies, which beat two double-buffered
+//     workgroups per CU by 12-24%;
 //   * v_mfma_f32_32x32x16_bf16 with B (the head's weight rows, n) as the first operand and A (rows r) as
 //     the second, so each lane holds 4 consecutive d of one row: 8-byte stores;
-//   * buffer resources bound every operand, so M / N tails read as zero and need no clamping.
+//   * buffer resources bound every operand (row offsets in the range-checked VGPR offset), so M / N tails
+//     read as zero and need no clamping.
 #include "kg_device.h"
 #include "kg_host.h"
 
@@ -42,10 +45,9 @@ KG_DEV v8bf kg_lds_bf16x8(const u8* p) {
   return r;
 }
 
-__global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Args p) {
+__global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Args p) {
   constexpr int BM = 128, BN = 128, TI = 2, TJ = 2, SA = BM * 128, STAGE = (BM + BN) * 128;
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -83,15 +85,17 @@ __global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Arg
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // A buffer load's range check covers its VGPR offset only: the row offsets go there (rows past the
+  // tile's live rows then read zeros), and only the K offset, which stays inside a row, in the scalar one.
   auto issue = [&](u8* stage, int kt) {
     const int ko = kt * 128;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int r = (wave * 4 + q) * 8;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * 4 + q) * 1024), 16, va,
-                                               (int)(r * p.a_rs) + ko, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * 4 + q) * 1024), 16, vb,
-                                               (int)(r * p.b_rs) + ko, 0, 0);
+      const unsigned r = (unsigned)((wave * 4 + q) * 8);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * 4 + q) * 1024), 16,
+                                               va + r * (unsigned)p.a_rs, ko, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * 4 + q) * 1024), 16,
+                                               vb + r * (unsigned)p.b_rs, ko, 0, 0);
     }
   };
   auto compute = [&](const u8* stage) {
@@ -110,24 +114,20 @@ __global__ __launch_bounds__(256, 2) void kg_bf16_batched_kernel(const KgBf16Arg
   };
 
   const int KT = p.k >> 6;
-  issue(st0, 0);
-  __syncthreads();
-  int kt = 0;
-  for (; kt + 2 <= KT; kt += 2) {
-    issue(st1, kt + 1);
+  // one stage: its DMA, a barrier once every wave's copy has landed, the MFMAs, a barrier before the
+  // next DMA overwrites it (the other workgroups on the CU fill the gaps)
+  for (int kt = 0; kt < KT; ++kt) {
+    issue(st0, kt);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     compute(st0);
     __syncthreads();
-    if (kt + 2 < KT) issue(st0, kt + 2);
-    compute(st1);
-    __syncthreads();
   }
-  if (kt < KT) compute(st0);
   kg_mfma_drain();
 
   // Epilogue through LDS: each wave stages its 64 x 64 outputs (rows m, 128-byte rows, 16-byte chunk c in
-  // slot c ^ (m & 7)) in stage 0, then stores 16 bytes per lane, 8 lanes per row: the 128-byte row pieces
-  // of D are whole cache lines (D's byte strides are multiples of 128 at the reference's shapes).
-  __syncthreads();                               // every wave is done with the stages
+  // slot c ^ (m & 7)) in the stage (free: the K loop ends with a barrier), then stores 16 bytes per lane,
+  // 8 lanes per row: the 128-byte row pieces of D are whole cache lines (D's byte strides are multiples of
+  // 128 at the reference's shapes).
   u8* const stg = st0 + wave * 8192;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
