@@ -452,19 +452,20 @@ KG_DEV KgPTile kg_ptile(const KgFp8Args& p, const int* tp, const int* ps, int to
 }
 
 // Where a tile's operands start: A rows from m0 (VGPR offset base), the expert's W panel (resource) and
-// the column tile's first W row (VGPR offset base).  Branch-free: an empty range stands for "no tile".
+// the column tile's first W row (VGPR offset base).  Branch-free: "no tile" (g < 0) is an A base past
+// every resource (KG_OOB) and an empty W resource, so its loads read zeros.
+constexpr unsigned KG_OOB = 0x80000000u;
 struct KgDmaSrc {
   __amdgpu_buffer_rsrc_t rw;
   unsigned abase, wbase;
-  int ok;                                      // 0: no tile (loads read zeros)
   int half;                                    // a tile of at most 128 rows: A rows 128.. are not loaded
 };
 
 KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
   KgDmaSrc d;
-  d.ok = t.g >= 0;
-  d.rw = kg_rsrc(p.w + (size_t)(t.g > 0 ? t.g : 0) * p.n * p.k, d.ok ? (long long)p.n * p.k : 0);
-  d.abase = (unsigned)(t.m0 * p.lda);
+  const bool ok = t.g >= 0;
+  d.rw = kg_rsrc(p.w + (size_t)(ok ? t.g : 0) * p.n * p.k, ok ? (long long)p.n * p.k : 0);
+  d.abase = ok ? (unsigned)(t.m0 * p.lda) : KG_OOB;
   d.wbase = (unsigned)(t.nt * cn * p.k);
   d.half = t.m_end - t.m0 <= 128;
   return d;
@@ -669,7 +670,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   const int KS = ((p.k + 511) >> 9) << 2;      // stages per tile (padded to a multiple of 4)
   const int KB = p.k >> 7;                     // live K blocks of 128
   const int half = p.n >> 1, kw = (p.k + 511) >> 9;
-  const __amdgpu_buffer_rsrc_t rnull = kg_rsrc(p.a, 0);
   const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a, (long long)p.rows * p.lda);
   const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
 
@@ -710,17 +710,18 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // for the whole DMA queue).
   const unsigned arow_w = (unsigned)(wave * 64) * (unsigned)p.lda;
   const unsigned wrow_w = (unsigned)kg_wrow<MODE, 256>(0, half, wave * 64) * (unsigned)p.k;
+  // A load with nothing to fetch (K padding, no tile, a half tile's A rows 128..) gets a row base past the
+  // resource (KG_OOB: the VGPR offset stays below 2^32, as 64 lda and 64 k are below 2^31), so it reads zeros.
   auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
-    const bool in = ko < p.k && d.ok;
     const int j = q & 7;
     unsigned v = q < 8 ? va[j & 1] : vw[j & 1];
-    unsigned u = q < 8 ? arow_w + d.abase : wrow_w + d.wbase;
+    unsigned u = q < 8 ? (d.half && wave >= 2 ? KG_OOB : arow_w + d.abase) : wrow_w + d.wbase;
+    if (ko >= p.k) u = KG_OOB;
     unsigned l = (unsigned)(wave * 8192);
     asm volatile("" : "+v"(v));
     v += u + (unsigned)(j * 8) * (unsigned)(q < 8 ? p.lda : p.k);
-    const __amdgpu_buffer_rsrc_t rs = q < 8 ? (in && !(d.half && wave >= 2) ? ra : rnull) : (in ? d.rw : rnull);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (KG_LDS void*)(st + (q < 8 ? 0 : SA) + l + j * 1024), 16, v, ko, 0,
-                                             0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(q < 8 ? ra : d.rw, (KG_LDS void*)(st + (q < 8 ? 0 : SA) + l + j * 1024), 16,
+                                             v, ko, 0, 0);
   };
   // Scale words of word row kg4 (the exponent bytes of K blocks 4 kg4 .. 4 kg4 + 3, byte kb & 3) of tile t;
   // the MFMA picks its byte with op_sel.  wa/wb[0] is the word group in use, [1] the next one, loaded two
@@ -991,7 +992,8 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
   // the persistent kernel's epilogue stores 16-byte chunks of 8 columns
   if (big >= 256 && n % 8 == 0 && ldc % 8 == 0 && kg_aligned(c, 16) && (long long)rows * ldc * 2 < (1ll << 31)) {
     p.m_tiles = (m + 255) / 256, p.n_tiles = (n + 255) / 256;
-    KG_CHECK(big < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+    KG_CHECK(big < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31) &&
+             256ll * lda < (1ll << 31));
     return kg_fp8_launch_persistent<0>(p, big, st);
   }
   p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
@@ -1013,7 +1015,8 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
   p.groups = groups;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n + 255) / 256;   // an upper bound of the live tiles
   const long long total = (long long)p.m_tiles * p.n_tiles;
-  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31) &&
+           256ll * lda < (1ll << 31));
   return kg_fp8_launch_persistent<1>(p, total, (hipStream_t)stream);
 }
 
@@ -1031,6 +1034,7 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   p.ldc = n, p.sfa_rows = sfa_rows, p.groups = groups, p.sf_rows = sf_rows;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n / 2) / 128;
   const long long total = (long long)p.m_tiles * p.n_tiles;
-  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31));
+  KG_CHECK(total < (1ll << 31) && (long long)rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31) &&
+           256ll * lda < (1ll << 31));
   return kg_fp8_launch_persistent<2>(p, total, (hipStream_t)stream);
 }
