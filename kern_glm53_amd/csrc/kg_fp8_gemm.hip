@@ -714,16 +714,25 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // resource (KG_OOB: the VGPR offset stays below 2^32, as 64 lda and 64 k are below 2^31), so it reads zeros.
   auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
     const int j = q & 7;
-    unsigned v = q < 8 ? va[j & 1] : vw[j & 1];
     unsigned u = q < 8 ? (d.half && wave >= 2 ? KG_OOB : arow_w + d.abase) : wrow_w + d.wbase;
     if (ko >= p.k) u = KG_OOB;
-    unsigned l = (unsigned)(wave * 8192);
-    asm volatile("" : "+v"(v));
-    v += u + (unsigned)(j * 8) * (unsigned)(q < 8 ? p.lda : p.k);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(q < 8 ? ra : d.rw, (KG_LDS void*)(st + (q < 8 ? 0 : SA) + l + j * 1024), 16,
-                                             v, ko, 0, 0);
-  };
-  // Scale words of word row kg4 (the exponent bytes of K blocks 4 kg4 .. 4 kg4 + 3, byte kb & 3) of tile t;
+    // The row step and the lane offset pass through an empty asm statement, so that the compiler forms the
+    // VGPR offset here rather than keeping 16 precomputed offsets per buffer in registers; the instruction's
+    // immediate offset (added to both the LDS and the memory address) places instructions j & 3, so only 4
+    // LDS bases per buffer remain.
+    unsigned v = q < 8 ? va[j & 1] : vw[j & 1];
+    unsigned rs = 8u * (unsigned)(q < 8 ? p.lda : p.k);
+    asm volatile("" : "+v"(v), "+v"(rs));
+    v += u + (unsigned)j * rs - (unsigned)((j & 3) * 1024);
+    u8* const m0 = st + (q < 8 ? 0 : SA) + wave * 8192 + (j & 4) * 1024;
+    const __amdgpu_buffer_rsrc_t r = q < 8 ? ra : d.rw;
+    switch (j & 3) {
+      case 0: __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KG_LDS void*)m0, 16, v, ko, 0, 0); break;
+      case 1: __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KG_LDS void*)m0, 16, v, ko, 1024, 0); break;
+      case 2: __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KG_LDS void*)m0, 16, v, ko, 2048, 0); break;
+      default: __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KG_LDS void*)m0, 16, v, ko, 3072, 0); break;
+    }
+  };  // Scale words of word row kg4 (the exponent bytes of K blocks 4 kg4 .. 4 kg4 + 3, byte kb & 3) of tile t;
   // the MFMA picks its byte with op_sel.  wa/wb[0] is the word group in use, [1] the next one, loaded two
   // stages before it is needed.
   u32 wa[2][TJ], wb[2][TI];
@@ -852,7 +861,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 
   // ---- prologue: the first word group, stage 0 and instructions 0..3 of stage 1 (as the ring has them
   // at a stage's start)
-  KgDmaSrc dsc = dsrc(cur);
+  KgDmaSrc dsc = dsrc(cur), dnx = dsrc(nxt);     // this tile's and the next tile's DMA sources
   words(cur, 0, wa[0], wb[0]);
   KG_ISSUE_ORDER();
 #pragma unroll
@@ -893,7 +902,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   const bool lastg = ks + 4 >= KS;                                                                         \
   const KgPTile wt = lastg ? nxt : cur;                                                                    \
   const int kn = lastg ? 0 : (ks + 4) * 128, wkg = lastg ? 0 : (ks >> 2) + 1;                              \
-  const KgDmaSrc dsn = dsrc(wt);                                                                           \
+  const KgDmaSrc dsn = lastg ? dnx : dsc;                                                                  \
   const int k0 = ks * 128
 #define KG_GROUP_END()                                                                                     \
   _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
@@ -928,10 +937,11 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     if (nidx < 0) break;
     ++round;
     cur = nxt;
-    dsc = dsrc(cur);
+    dsc = dnx;
     nidx = kg_round_tile(round + 1, live);
     nxt.g = -1;
     if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
+    dnx = dsrc(nxt);
   }
   __builtin_amdgcn_s_waitcnt(0);
 #undef KG_PSTAGE
