@@ -26,7 +26,10 @@ extern "C" {
  *   C[r][0:n] = bf16( sum_kb 2^(sfa[r,kb]-127) 2^(sfb[c,kb]-127) sum_{k in kb} A[r][k] W[c][k] ), r < m,
  * f32 accumulation.  a: e4m3 [rows][lda]; w: e4m3 [n][k]; sfa: words [k/512][sfa_rows]; sfb: words
  * [k/512][n] (one word per weight row); c: bf16 [rows][ldc], columns [n, ldc) untouched.
- * Requires k % 128 == 0, m <= rows <= sfa_rows, n <= ldc, k <= lda, lda % 16 == 0, ldc % 4 == 0. */
+ * Requires k % 128 == 0, m <= rows <= sfa_rows, n <= ldc, k <= lda, lda % 16 == 0, ldc % 4 == 0, a and w
+ * 16-byte aligned, c 8-byte aligned; with 256 or more tiles of 256 x 256 (the persistent kernel, taken
+ * when n % 8 == 0, ldc % 8 == 0 and c is 16-byte aligned) also rows * lda, n * k, 256 * lda and
+ * rows * ldc * 2 below 2^31 (the byte ranges of its buffer resources). */
 int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, void* c, int m, int n, int k,
                 int rows, int lda, int ldc, int sfa_rows, void* stream);
 
@@ -35,7 +38,8 @@ int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, 
  * for every group g, rows [round_up128(psum[g-1]), psum[g]) of C (psum[-1] = 0) are the dense GEMM of
  * the same rows of A with weight rows [g n, (g+1) n) and scale words [g k/512, (g+1) k/512).  Rows no group
  * owns are left untouched.  psum: device int32 [groups] (glm_moe_psum's output).  Requires n % 8 == 0,
- * ldc % 8 == 0, c 16-byte aligned, rows % 128 == 0, k % 128 == 0, lda % 16 == 0. */
+ * ldc % 8 == 0, c 16-byte aligned, a and w 16-byte aligned, rows % 128 == 0, k % 128 == 0, lda % 16 == 0,
+ * groups <= 1024, and rows * lda, n * k, 256 * lda, rows * ldc * 2 below 2^31. */
 int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, const void* sfb, void* c, const int* psum,
                      int groups, int n, int k, int rows, int lda, int ldc, int sfa_rows, void* stream);
 
@@ -43,7 +47,8 @@ int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, const void* 
  * `fp8.moe.gu` + `silu_moe` of scripts/gen.py:442-443 (source/glm_glue.cu:177-194) in one launch.  With
  * I = n / 2 (columns [0, I) gate, [I, 2I) up of every expert's weight rows), every live row r writes
  * q[r][0:I] = e4m3(bf16(silu(g) u) / 2^(e-127)) and its exponent bytes into sf words [I/512][sf_rows];
- * rows no group owns are untouched.  No bf16 gate_up buffer is written.  Requires n % 256 == 0. */
+ * rows no group owns are untouched.  No bf16 gate_up buffer is written.  Requires n % 256 == 0, q, a and w
+ * 16-byte aligned, and the psum variant's size limits (with rows * n / 2 below 2^31). */
 int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, const void* sfb, const int* psum,
                                 int groups, int n, int k, int rows, int lda, int sfa_rows, void* q, void* sf,
                                 int sf_rows, void* stream);

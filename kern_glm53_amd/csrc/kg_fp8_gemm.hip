@@ -1,26 +1,24 @@
 // fp8 1d1d GEMMs of kern-glm53's `glm_deepgemm` path on gfx950: e4m3 x e4m3 with UE8M0 128-K-block
-// scales on both operands, f32 accumulation, bf16 out (source/glm_deepgemm.cu:17-24, 38-41;
-// scripts/glm_ops.py:57-78).  One kernel template, three modes:
-//   MODE 0  dense:    C[0:m, 0:n] = A . W^T
+// scales on both operands, f32 accumulation (source/glm_deepgemm.cu:17-24, 38-41; scripts/glm_ops.py:57-78).
+// The persistent 256 x 256 kernel serves three modes:
+//   MODE 0  dense:    C[0:m, 0:n] = A . W^T, bf16 out
 //   MODE 1  psum:     per expert g, rows [round_up128(psum[g-1]), psum[g]) with W rows [g n, (g+1) n)
 //   MODE 2  psum + SiLU-mul + per-128 e4m3 requant epilogue (gate columns [0, n/2), up [n/2, n))
+// and a 128 x 128 one-tile-per-workgroup kernel takes dense GEMMs too small for it.
 //
-// Design (CDNA4):
-//   * 256 threads = 4 wave64s in a 2 x 2 grid; a wave owns (BM/2) x (BN/2) outputs as 32x32 tiles of
+// Shared design (CDNA4):
+//   * 256 threads = 4 wave64s in a 2 x 2 grid; a wave owns a quarter of the tile as 32x32 tiles of
 //     v_mfma_scale_f32_32x32x64_f8f6f4.  The weight tile is the MFMA's first operand (rows = n) and the
-//     activation tile its second (columns = m), so a lane ends up with 4 consecutive n of one row m:
-//     8-byte bf16 stores.  The UE8M0 exponent bytes go straight into the MFMA's scale operands (the
-//     128-K block scale is constant over the instruction's 64 K), so no per-block rescaling in VALU.
-//   * K advances 128 at a time (one scale block).  Both operand tiles of a K step are copied HBM -> LDS
-//     with global_load_lds_dwordx4 (no VGPR staging), 128-byte rows, the 16-byte chunk index XORed with
-//     (row & 7) so that MFMA fragment reads (8 rows x 16 B per ds_read_b128 phase) hit 32 distinct banks.
-//     Two stages live in two distinct __shared__ arrays (the K loop unrolled by two), so the compiler
-//     knows the DMA into one stage never aliases the fragment reads of the other.
+//     activation tile its second (columns = m), so a lane ends up with 4 consecutive n of one row m.  The
+//     UE8M0 exponent bytes go straight into the MFMA's scale operands (op_sel picks the byte of the
+//     packed word), so dequantization happens inside the MFMA.
+//   * K advances 128 (one scale block) per stage.  Both operand tiles go HBM -> LDS by buffer_load ... lds
+//     (no VGPR staging) into 128-byte rows, 16-byte chunk c of row r in slot c ^ ((r >> 1) & 7): the 16 rows
+//     of a ds_read_b128 phase cover the 64 banks once, and every 8 DMA lanes read one whole 128-byte line.
+//     Stages live in distinct __shared__ arrays, so the compiler knows a DMA into one never aliases the
+//     fragment reads of the other.
 //   * Workgroup ids are remapped so each XCD (its own L2) gets a contiguous range of output tiles, walked
-//     in groups of 8 M tiles (dense) or row-block-major (grouped: the 16-32 N tiles of one expert's row
-//     block run together and share its A rows; consecutive row blocks of an expert share its W panel).
-//   * Grouped modes map a 128-row block to its expert by a binary search of psum in LDS: experts start
-//     128-aligned, so block b simply covers rows [128 b, 128 b + 128) and only live blocks do work.
+//     in groups of 8 row tiles, column-tile-major inside a group.
 #include "kg_device.h"
 #include "kg_host.h"
 
@@ -132,16 +130,16 @@ KG_DEV void kg_fp8_epilogue(const KgFp8Args& p, v16f (&acc)[BN / 64][BM / 64], i
   }
 }
 
-template <int BM, int BN, int MODE>
-__global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) {
+// Dense GEMMs too small for the persistent kernel (fewer than 256 tiles of 256 x 256) or whose output
+// strides it cannot store: one 128 x 128 tile per workgroup, K blocks of 128 through two LDS stages.
+__global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
+  constexpr int BM = 128, BN = 128;
   constexpr int TJ = BM / 64;            // m tiles (32 rows) per wave  -> MFMA operand B
   constexpr int TI = BN / 64;            // n tiles (32 cols) per wave  -> MFMA operand A
   constexpr int NQA = BM / 32, NQB = BN / 32;   // 1 KB DMA instructions per wave per stage
   constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;
-  static_assert(MODE != 2 || BN == 256, "the fused epilogue quantizes 128 output columns per workgroup");
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
-  __shared__ int ps[1024], tp[1024], wtot[4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -150,89 +148,20 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   // Tile order: groups of G = 8 row tiles, column-tile-major inside a group, so the ~32 workgroups an XCD
   // runs at once share 8 A row tiles and ~4 weight column slices through its L2.
   constexpr int G = 8;
-  int nt, g = 0, m0, m_end;
-  if constexpr (MODE == 0) {
-    const int wid = kg_xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int gsz = G * p.n_tiles, grp = wid / gsz, first = grp * G;
-    const int gm = min(p.m_tiles - first, G), r = wid - grp * gsz;
-    nt = r / gm;
-    m0 = (first + r % gm) * BM;
-    m_end = min(p.m, m0 + BM);
-  } else {
-    // Expert g owns rows [start_g, psum[g]) with start_g = round_up128(psum[g-1]) and needs
-    // R_g = ceil(rows_g / BM) row tiles.  An exclusive prefix tp[] of R_g (a block-wide scan: each thread
-    // sums four experts, wave shuffles scan the 256 partials) numbers the live row tiles 0..total-1.
-    // Only the first total * n_tiles workgroups work; they are spread over the XCDs as in the dense case
-    // and ordered expert by expert, each expert's tiles grouped as above, so the workgroups that share
-    // an expert's weight slice run side by side on one XCD.
-    int part = 0;
-    int tl[4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int e = tid * 4 + x;
-      int t = 0;
-      if (e < p.groups) {
-        const int end = p.psum[e];
-        const int start = e ? ((p.psum[e - 1] + 127) >> 7) << 7 : 0;
-        ps[e] = end;
-        t = end > start ? (end - start + BM - 1) / BM : 0;
-      }
-      tl[x] = t;
-      part += t;
-    }
-    const int lane_ = tid & 63, w_ = tid >> 6;
-    int incl = part;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o, 64);
-      if (lane_ >= o) incl += v;
-    }
-    if (lane_ == 63) wtot[w_] = incl;
-    __syncthreads();
-    int base = incl - part;
-    for (int v = 0; v < w_; ++v) base += wtot[v];
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int e = tid * 4 + x;
-      if (e < p.groups) tp[e] = base;
-      base += tl[x];
-    }
-    const int total = wtot[0] + wtot[1] + wtot[2] + wtot[3];
-    __syncthreads();
-    const int live = total * p.n_tiles;
-    if ((int)blockIdx.x >= live) return;       // past the live tiles (uniform exit)
-    const int wid = kg_xcd_remap((int)blockIdx.x, live);
-    const int rt_flat = wid / p.n_tiles;
-    int lo = 0, hi = p.groups - 1;             // the last g with tp[g] <= rt_flat (it has R_g > 0)
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (tp[mid] <= rt_flat) lo = mid; else hi = mid - 1;
-    }
-    g = lo;
-    const int rg = (g + 1 < p.groups ? tp[g + 1] : total) - tp[g];
-    const int l = wid - tp[g] * p.n_tiles, grp = l / (G * p.n_tiles);
-    const int gm = min(rg - grp * G, G), r = l - grp * G * p.n_tiles;
-    nt = r / gm;
-    const int start = g ? ((ps[g - 1] + 127) >> 7) << 7 : 0;
-    m0 = start + (grp * G + r % gm) * BM;
-    m_end = min(min(ps[g], p.rows), m0 + BM);   // rows past the buffer are never touched
-    // values read from LDS are per-lane to the compiler; declaring them uniform keeps the buffer
-    // resources built from them in SGPRs (otherwise every buffer load becomes a waterfall loop)
-    g = __builtin_amdgcn_readfirstlane(g);
-    nt = __builtin_amdgcn_readfirstlane(nt);
-    m0 = __builtin_amdgcn_readfirstlane(m0);
-    m_end = __builtin_amdgcn_readfirstlane(m_end);
-    if (m0 >= m_end) return;
-  }
-  const int n0 = nt * (MODE == 2 ? BN / 2 : BN);
+  const int wid = kg_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int gsz = G * p.n_tiles, grp = wid / gsz, first = grp * G;
+  const int gm = min(p.m_tiles - first, G), r = wid - grp * gsz;
+  const int nt = r / gm;
+  const int m0 = (first + r % gm) * BM;
+  const int m_end = min(p.m, m0 + BM);
+  const int n0 = nt * BN;
   const int kw = (p.k + 511) >> 9, KT = p.k >> 7;
-  const int half = p.n >> 1;                 // mode 2: I
 
   // ---- buffer resources: rows past the live range read as zero, so no per-lane clamping
   const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a + (size_t)m0 * p.lda, (long long)(m_end - m0) * p.lda);
-  const __amdgpu_buffer_rsrc_t rw = kg_rsrc(p.w + (size_t)g * p.n * p.k, (long long)p.n * p.k);
+  const __amdgpu_buffer_rsrc_t rw = kg_rsrc(p.w, (long long)p.n * p.k);
   const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
-  const __amdgpu_buffer_rsrc_t rsb = kg_rsrc(p.sfb + (size_t)g * kw * p.n, (long long)kw * p.n * 4);
+  const __amdgpu_buffer_rsrc_t rsb = kg_rsrc(p.sfb, (long long)kw * p.n * 4);
   // NQA and NQB are even and every wave starts at an even instruction, so instruction q's rows start at
   // 8 * (even + q): row r = 8 * (that) + (lane >> 3) has (r >> 1) & 7 = ((q & 1) << 2) | (lane >> 4)
   static_assert(NQA % 2 == 0 && NQB % 2 == 0, "DMA swizzle parity");
@@ -247,11 +176,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
   // ---- per-lane LDS fragment offsets and scale word offsets.  Every fragment row is (lane & 31) plus a
   // multiple of 32, so its swizzle is (chunk ^ ((lane & 31) >> 1 & 7)) and tile offsets are immediates.
   const int arow0 = wm * (BM / 2) + (lane & 31);               // activation rows: + 32 j
-  const int wbase = MODE == 2 ? wn * (BN / 4) : wn * (BN / 2);  // weight rows: + wtile(i)
-  auto wtile = [](int i) -> int {
-    if constexpr (MODE == 2) return i < TI / 2 ? i * 32 : BN / 2 + (i - TI / 2) * 32;
-    else return i * 32;
-  };
+  const int wbase = wn * (BN / 2);                             // weight rows: + 32 i
+  auto wtile = [](int i) -> int { return i * 32; };
   unsigned offa[2][2], offw[2][2];
 #pragma unroll
   for (int kh = 0; kh < 2; ++kh)
@@ -263,7 +189,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
     }
   unsigned sb_off[TI];
 #pragma unroll
-  for (int i = 0; i < TI; ++i) sb_off[i] = (unsigned)kg_wrow<MODE, BN>(n0, half, wbase + wtile(i) + (lane & 31)) * 4u;
+  for (int i = 0; i < TI; ++i) sb_off[i] = (unsigned)(n0 + wbase + wtile(i) + (lane & 31)) * 4u;
   const unsigned sa_off = (unsigned)(m0 + arow0) * 4u;
 
   v16f acc[TI][TJ];
@@ -276,7 +202,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_kernel(const KgFp8Args p) 
 
   int woff[NQB];   // byte offset (K = 0) of the first weight row of each of this wave's W DMA instructions
 #pragma unroll
-  for (int q = 0; q < NQB; ++q) woff[q] = kg_wrow<MODE, BN>(n0, half, (wave * NQB + q) * 8) * p.k;
+  for (int q = 0; q < NQB; ++q) woff[q] = (n0 + (wave * NQB + q) * 8) * p.k;
 
   // ---- software-pipelined main loop (one K block of 128 per step, two LDS stages).
   // The MFMAs of a K half run as NO rows x NI columns: the "inner" operand's NI fragments stay in
@@ -954,14 +880,12 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 
 // ---------------------------------------------------------------- host entry points
 
-template __global__ void kg_fp8_gemm_kernel<128, 128, 0>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_persistent<0>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_persistent<1>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_persistent<2>(const KgFp8Args);
 
-template <int BM, int BN, int MODE>
-static int kg_fp8_launch(KgFp8Args& p, int total, hipStream_t st) {
-  hipLaunchKernelGGL((kg_fp8_gemm_kernel<BM, BN, MODE>), dim3(total), dim3(256), 0, st, p);
+static int kg_fp8_launch_tile(KgFp8Args& p, int total, hipStream_t st) {
+  hipLaunchKernelGGL(kg_fp8_gemm_tile, dim3(total), dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
@@ -1007,7 +931,7 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
     return kg_fp8_launch_persistent<0>(p, big, st);
   }
   p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
-  return kg_fp8_launch<128, 128, 0>(p, p.m_tiles * p.n_tiles, st);
+  return kg_fp8_launch_tile(p, p.m_tiles * p.n_tiles, st);
 }
 
 extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, const void* sfb, void* c,
@@ -1036,7 +960,8 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   KG_CHECK(a && w && sfa && sfb && psum && q && sf && groups >= 1 && groups <= 1024);
   KG_CHECK(n > 0 && n % 256 == 0 && k > 0 && k % 128 == 0 && rows > 0 && rows % 128 == 0 && rows <= sfa_rows &&
            rows <= sf_rows && k <= lda);
-  KG_CHECK(lda % 16 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(q, 4));
+  KG_CHECK(lda % 16 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(q, 16));
+  KG_CHECK((long long)rows * (n / 2) < (1ll << 31));
   KG_CHECK(kg_aligned(sfa, 4) && kg_aligned(sfb, 4));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb;
