@@ -247,8 +247,9 @@ def time_launch(fn, stream, iters=5):
     return e0.elapsed_time(e1) / iters
 
 
-def cpu_baseline(data, rows=2048, runs=3):
-    """The oracle's fp32 dequantize-then-matmul (PyTorch-CPU) on rows [0, rows) of each dense GEMM."""
+def cpu_baseline(data, rows=8192, runs=5):
+    """The oracle's fp32 dequantize-then-matmul (PyTorch-CPU) on rows [0, rows) of each dense GEMM: a bounded
+    sample of about 10 s of CPU work (half of the M = 16384 chunk, five runs)."""
     from oracle import ref
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
