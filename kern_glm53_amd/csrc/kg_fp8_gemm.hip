@@ -398,11 +398,11 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 }
 
 // Epilogue of the persistent kernel for modes 0 and 1: bf16 through LDS, so that each store writes 16
-// contiguous bytes per lane and 16 lanes cover a 256-byte row segment.  Per m tile j (32 rows), each wave
-// stages its 32 x 128 outputs (8 KB) in `stage`: the 64 weight rows of the last stage's buffer that only
-// this wave's DMA writes, and not before the next tile's first stage (so no other wave touches them).
-// Rows are 256 bytes; chunk c (8 columns) of row m sits in slot c ^ (m & 15), with its two 8-byte halves
-// swapped when m & 16, which makes the 8-byte writes of a wave's 32 rows conflict-free.
+// contiguous bytes per lane and 16 lanes cover a 256-byte row segment.  `stage` is the wave's own 4 KB:
+// each 32-row MFMA tile j goes through it in two halves of 16 rows (256 bytes each; chunk c of 8 columns
+// of row m in slot c ^ m, which makes both the 8-byte writes of the half's 16 rows and the 16-byte reads
+// conflict-free).  Every wave issues exactly 32 stores per tile, which the next tile's first barrier
+// leaves in flight.
 KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int m0, int m_end,
                                 int n0, int wm, int wn, bool half) {
   // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
@@ -410,46 +410,40 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
   int lane;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
   const __amdgpu_buffer_rsrc_t rc = kg_rsrc(p.c, (long long)p.rows * p.ldc * 2);
-  u8* const lo = stage;                          // rows 0..15 of the wave's staging
-  u8* const hi = stage + 4096;                   // rows 16..31
-  const int mr = lane & 31;                       // this lane's row when writing
-  u8* const wrow = (mr < 16 ? lo : hi) + (mr & 15) * 256;
-  const int hsel = (lane >> 5) ^ ((lane >> 4) & 1);
+  const int mr = lane & 31;                       // this lane's row of the MFMA tile
+  u8* const wrow = stage + (mr & 15) * 256 + ((lane >> 5) << 3);
   const int rbase = m0 + (half ? wm * 64 : wm * 128);   // a half tile's waves own 64 rows each
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool jv = !half || j < 2;               // a half tile has two m tiles per wave
-    if (jv) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int hh = 0; hh < 2; ++hh) {
+      if (jv && (mr >> 4) == hh) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int c = i * 4 + rr;
-          uint2 o;
-          o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
-          o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
-          *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4) + (hsel << 3)) = o;
-        }
-      __builtin_amdgcn_s_waitcnt(0xc07f);         // lgkmcnt(0): this wave's writes are in LDS
-    }
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int idx = t * 64 + lane, m = idx >> 4, c = idx & 15;
-      const u8* rrow = (m < 16 ? lo : hi) + (m & 15) * 256;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (jv) v = *reinterpret_cast<const uint4*>(rrow + ((c ^ (m & 15)) << 4));
-      if (m & 16) {
-        const unsigned x = v.x, y = v.y;
-        v.x = v.z, v.y = v.w, v.z = x, v.w = y;
+          for (int rr = 0; rr < 4; ++rr) {
+            const int c = i * 4 + rr;
+            uint2 o;
+            o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+            o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+            *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4)) = o;
+          }
       }
-      const int gm = rbase + j * 32 + m, gn = n0 + wn * 128 + c * 8;
-      // always issued (no branch); lanes outside the tile's rows or columns get an offset past the
-      // resource, which drops the write
-      const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
-      __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
-      __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);         // lgkmcnt(0): this wave's writes are in LDS
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int idx = t * 64 + lane, m = idx >> 4, c = idx & 15;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + m * 256 + ((c ^ m) << 4));
+        const int gm = rbase + j * 32 + hh * 16 + m, gn = n0 + wn * 128 + c * 8;
+        // always issued (no branch); lanes outside the tile's rows or columns get an offset past the
+        // resource, which drops the write
+        const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
+        __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
+        __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);         // reads done before the next half's writes
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);           // reads done before the next m tile's writes
   }
 }
 
@@ -541,6 +535,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   __shared__ int ps[MODE == 0 ? 1 : 1024], tp[MODE == 0 ? 1 : 1024], wtot[4];
   __shared__ float xam[MODE == 2 ? 2 : 1][BM];
   __shared__ u8 xe[MODE == 2 ? BM : 1];
+  __shared__ __attribute__((aligned(1024))) u8 stg[MODE == 2 ? 16 : 16384];   // modes 0/1 epilogue staging
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -663,8 +658,13 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // stages before it is needed.
   u32 wa[2][TJ], wb[2][TI];
   auto words = [&](const KgPTile& t, int kg4, u32* xa, u32* xb) {
+    // the lane id from a volatile read: the per-lane word offsets are formed here rather than kept in
+    // registers across the K loop (spilled, their reloads would wait for the whole DMA queue)
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
     const __amdgpu_buffer_rsrc_t rsb =
         kg_rsrc(p.sfb + (size_t)(t.g > 0 ? t.g : 0) * kw * p.n, t.g >= 0 ? (long long)kw * p.n * 4 : 0);
+    const int arow0 = wm * (BM / 2) + (ln & 31);
     const int arow = t.m_end - t.m0 <= 128 ? arow0 - wm * 64 : arow0;   // a half tile's wave rows
     const unsigned sa_off = (unsigned)((t.m0 + arow) * 4 + kg4 * p.sfa_rows * 4);
     const int n0 = t.nt * CN;
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
     for (int i = 0; i < TI; ++i)
       xb[i] = __builtin_amdgcn_raw_buffer_load_b32(
-          rsb, (unsigned)(kg_wrow<MODE, 256>(n0, half, wbase + wtile(i) + (lane & 31)) * 4 + kg4 * p.n * 4), 0, 0);
+          rsb, (unsigned)(kg_wrow<MODE, 256>(n0, half, wbase + wtile(i) + (ln & 31)) * 4 + kg4 * p.n * 4), 0, 0);
   };
 
   v16f acc[TI][TJ];
@@ -689,6 +689,25 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     asm volatile("" ::: "memory");                                                                        \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
   } while (0)
+  // DMA schedule: in mode 2 instructions 0..3 of stage s + 2 go out right after stage s's barrier and
+  // 4..15 during stage s + 1 (its epilogue stages in the weight rows of the last stage's buffer, which must
+  // stay untouched until the next tile's first stage); in modes 0/1 all 16 go out after the barrier, so a
+  // tile's epilogue stores follow the whole DMA of the next tile's stage 1 (its staging is its own LDS).
+  constexpr int NPRE = 4;
+  // A stage's barrier: this wave's DMA of stage s + 1 has landed (everything but, on PH 2, the 8 scale words
+  // issued after it), and every wave is done with this stage's buffer.  The first PH 0 after a modes 0/1
+  // epilogue leaves its 32 stores per wave in flight (vmcnt 32: they are the newest).
+#define KG_STAGE_BARRIER(PH, FIRST)                                                                        \
+  do {                                                                                                    \
+    if constexpr ((PH) == 2) {                                                                             \
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");                            \
+    } else if constexpr ((FIRST) && MODE != 2) {                                                           \
+      if (stores_pending) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");       \
+      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                       \
+    } else {                                                                                              \
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                            \
+    }                                                                                                     \
+  } while (0)
   // One stage s (PH = its index in the group of four = the byte of the scale words): 2 K halves x 16
   // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  Slots 0..11 issue DMA
   // instructions 4..15 of stage s + 1 into OTH (D1 / K1), one per MFMA; slots 1..4 read the second K
@@ -697,7 +716,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 12 after it),
   // publishes it and frees CUR: slots 26..29 issue instructions 0..3 of stage s + 2 into CUR (D2 / K2),
   // slots 26..30 read stage s + 1's first fragments from OTH.
-#define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2)                                                            \
+#define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                     \
   do {                                                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
     _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
@@ -707,7 +726,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
                                                                       (PH), (int)wb[0][o], (PH),          \
                                                                       (int)wa[0][n]);                     \
-          if (t_ < 12) dma1(OTH, D1, K1, 4 + t_);                                                          \
+          if (t_ < 16 - NPRE && !((FIRST) && MODE != 2)) dma1(OTH, D1, K1, NPRE + t_);                     \
           if (t_ == 12 && (PH) == 2) {                                                                     \
             KG_ISSUE_ORDER();                                                                             \
             words(wt, wkg, wa[1], wb[1]);                                                                 \
@@ -716,11 +735,11 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (kh == 0 && t_ >= 1 && t_ <= 4) res[1][t_ - 1] = KG_PFRAG_A(CUR, 1, t_ - 1);                  \
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
-          if (t_ == 25) {                                                                                 \
-            if constexpr ((PH) == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); \
-            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                 \
+          if (t_ == 25) KG_STAGE_BARRIER(PH, FIRST);                                                       \
+          if (t_ >= 26) {                                                                                 \
+            _Pragma("unroll") for (int q_ = 0; q_ < 16; ++q_)                                              \
+              if (q_ < NPRE && q_ * 6 / NPRE == t_ - 26) dma1(CUR, D2, K2, q_);                            \
           }                                                                                               \
-          if (t_ >= 26 && t_ <= 29) dma1(CUR, D2, K2, t_ - 26);                                            \
           if (t_ == 26) res[0][0] = KG_PFRAG_A(OTH, 0, 0);                                                 \
           if (t_ == 27) res[0][1] = KG_PFRAG_A(OTH, 0, 1);                                                 \
           if (t_ == 28) str[0] = KG_PFRAG_W(OTH, 0, 0);                                                    \
@@ -737,7 +756,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // t = 8 kh + 2 o + n.  The same 16 DMA instructions per stage, two per slot: 4..15 of stage s + 1 in
   // slots 0..5, 0..3 of stage s + 2 in slots 14, 15; the last read of CUR is at slot 12, the barrier
   // after slot 13; the words go out at slot 6 of PH 2.
-#define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2)                                                           \
+#define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                    \
   do {                                                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
     _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
@@ -747,9 +766,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
                                                                       (PH), (int)wb[0][o], (PH),          \
                                                                       (int)wa[0][n]);                     \
-          if (t_ < 6) {                                                                                   \
-            dma1(OTH, D1, K1, 4 + 2 * t_);                                                                \
-            dma1(OTH, D1, K1, 5 + 2 * t_);                                                                \
+          if (2 * t_ < 16 - NPRE && !((FIRST) && MODE != 2)) {                                            \
+            dma1(OTH, D1, K1, NPRE + 2 * t_);                                                             \
+            dma1(OTH, D1, K1, NPRE + 1 + 2 * t_);                                                         \
           }                                                                                               \
           if (t_ == 6 && (PH) == 2) {                                                                      \
             KG_ISSUE_ORDER();                                                                             \
@@ -759,13 +778,10 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (kh == 0 && t_ >= 1 && t_ <= 2) res[1][t_ - 1] = KG_PFRAG_AH(CUR, 1, t_ - 1);                 \
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
-          if (t_ == 13) {                                                                                 \
-            if constexpr ((PH) == 2) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); \
-            else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                 \
-          }                                                                                               \
+          if (t_ == 13) KG_STAGE_BARRIER(PH, FIRST);                                                       \
           if (t_ >= 14) {                                                                                 \
-            dma1(CUR, D2, K2, 2 * (t_ - 14));                                                             \
-            dma1(CUR, D2, K2, 2 * (t_ - 14) + 1);                                                         \
+            _Pragma("unroll") for (int q_ = 0; q_ < NPRE / 2; ++q_)                                        \
+              dma1(CUR, D2, K2, (t_ - 14) * (NPRE / 2) + q_);                                             \
           }                                                                                               \
           if (t_ == 14) {                                                                                 \
             res[0][0] = KG_PFRAG_AH(OTH, 0, 0);                                                           \
@@ -793,9 +809,11 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
   for (int q = 0; q < 16; ++q) dma1(st0, dsc, 0, q);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) dma1(st1, dsc, 128, q);
+  for (int q = 0; q < (MODE == 2 ? NPRE : 16); ++q) dma1(st1, dsc, 128, q);
   KG_ISSUE_ORDER();
-  asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  if constexpr (MODE == 2) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  bool stores_pending = false;                  // modes 0/1: the previous tile's epilogue stores in flight
 
   for (;;) {
     const bool halft = cur.m_end - cur.m0 <= 128;
@@ -834,32 +852,58 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
   _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i]
     if (halft) {
-      for (int ks = 0; ks < KS; ks += 4) {
+      {                                          // the first group: its stage 0 follows an epilogue
+        const int ks = 0;
         KG_GROUP_START();
-        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
-        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
-        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn);
-        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128);
+        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
+        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
+        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
+        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_GROUP_END();
+      }
+      for (int ks = 4; ks < KS; ks += 4) {
+        KG_GROUP_START();
+        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 0);
+        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
+        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
+        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
         KG_GROUP_END();
       }
     } else {
-      for (int ks = 0; ks < KS; ks += 4) {
+      {                                          // the first group: its stage 0 follows an epilogue
+        const int ks = 0;
         KG_GROUP_START();
-        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
-        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
-        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn);
-        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128);
+        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
+        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
+        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
+        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_GROUP_END();
+      }
+      for (int ks = 4; ks < KS; ks += 4) {
+        KG_GROUP_START();
+        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 0);
+        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
+        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
+        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
         KG_GROUP_END();
       }
     }
 #undef KG_GROUP_START
 #undef KG_GROUP_END
     kg_mfma_drain();
-    // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
-    if constexpr (MODE == 2)
+    if constexpr (MODE == 2) {
+      // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
       kg_fp8_epilogue_silu(p, acc, st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
-    else
-      kg_fp8_epilogue_lds(p, acc, st1 + SA + wave * 8192, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
+    } else {
+      // the rest of the next tile's stage 1 goes out before the stores, which then stay in flight across
+      // that tile's first barrier (its first stage issues none of it)
+      KG_ISSUE_ORDER();
+#pragma unroll
+      for (int q = NPRE; q < 16; ++q) dma1(st1, dnx, 128, q);
+      KG_ISSUE_ORDER();
+      kg_fp8_epilogue_lds(p, acc, stg + wave * 4096, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
+      stores_pending = true;
+    }
     if (nidx < 0) break;
     ++round;
     cur = nxt;
@@ -870,6 +914,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     dnx = dsrc(nxt);
   }
   __builtin_amdgcn_s_waitcnt(0);
+#undef KG_STAGE_BARRIER
 #undef KG_PSTAGE
 #undef KG_PSTAGEH
 #undef KG_PFRAG_AH
