@@ -58,6 +58,9 @@ def check(out_bits, ref32, abs_sum, k, what, window=None):
     (4096, 4096, 512, 4096, 512, 4096, 4096),       # 256 x 256 tiles
     (4000, 4160, 640, 4096, 640, 4224, 4096),       # 256 x 256 tiles, M and N tails, odd K-block count
     (4100, 4096, 1536, 4224, 1536, 4096, 4224),     # an M tail of 4 rows (half tiles), K = 3 x 512
+    (4096, 4096, 128, 4096, 128, 4096, 4096),       # one K block: three padded stages of four
+    (4352, 4224, 896, 4352, 896, 4232, 4352),       # 17 x 17 tiles, N tail of 128, ldc > n, K = 7 blocks
+    (8192, 2048, 2560, 8192, 2560, 2048, 8192),     # K = 5 groups of four stages
     (512, 256, 384, 512, 384, 256, 512),            # odd K-block count, 128 x 128 tiles
     (1, 2048, 6144, 16, 6144, 2048, 16),            # a single row
 ])
@@ -125,6 +128,31 @@ def test_fp8_gemm_psum(n, k):
     out = h(c, np.uint16)
     owned = ~torch.isnan(ref32[:, 0]).numpy()
     check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum n={n} k={k}", Wb[owned])
+    assert np.all(out[~owned] == SENTINEL)
+
+
+@pytest.mark.parametrize("groups,seed", [(8, 61), (1024, 62)])
+def test_fp8_gemm_psum_groups(groups, seed):
+    """Other expert counts: 8 large groups (many full row tiles per expert, several tiles per CU), and the
+    maximum of 1024 with most groups empty and tails of every size."""
+    n, k = 256, 512
+    rng = np.random.default_rng(seed)
+    if groups == 8:
+        counts = np.array([2300, 0, 129, 4097, 511, 1, 768, 1500], np.int32)
+    else:
+        counts = np.where(rng.random(groups) < 0.3, rng.integers(1, 400, groups), 0).astype(np.int32)
+    psum = ref.moe_psum(counts, groups)
+    rows = int((psum[-1] + 127) // 128 * 128) + 256
+    a, sfa = quant_act(rows, k, rows, k, rows, seed=seed)
+    w, sfb = quant_weight(n, k, seed=seed + 1, groups=groups)
+    ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows, abs_too=True)
+    Wb = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
+    c = filled((rows, n), SENTINEL, torch.int16)
+    ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows,
+                      groups=groups)
+    out = h(c, np.uint16)
+    owned = ~torch.isnan(ref32[:, 0]).numpy()
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum groups={groups}", Wb[owned])
     assert np.all(out[~owned] == SENTINEL)
 
 
