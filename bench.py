@@ -183,6 +183,50 @@ def glue_launches(data):
     ]
 
 
+def producer_launches(data, dev):
+    """The operand producers upstream of the GEMMs at the M = 16384 chunk (scripts/gen.py:360-378, 405):
+    (name, launch, algorithmic HBM bytes).  Inputs are the bench's own GEMM outputs where the reference
+    chains them (q_a/kv_a's C is mla_prep's x, q_b's C is q_post's qb); the caches hold 65536 slots."""
+    from kern_glm53_amd import ops, synth
+
+    g = synth.generator(901, "cuda")
+    bf = lambda *s: (torch.randn(*s, generator=g, device=dev)).to(torch.bfloat16)
+    ctx = 65536
+    p = {"h": bf(M, H), "res": bf(M, H), "gamma": (1 + 0.1 * torch.randn(H, generator=g, device=dev)).bfloat16(),
+         "xn": torch.empty(M, H, dtype=torch.bfloat16, device=dev), "xq": torch.empty(M, H, dtype=torch.uint8, device=dev),
+         "xsf": torch.empty(ops.sf_words(H) * M * 4, dtype=torch.uint8, device=dev)}
+    inv = 8e6 ** (-torch.arange(32, device=dev, dtype=torch.float64) / 32)
+    ang = torch.arange(ctx, device=dev, dtype=torch.float64)[:, None] * inv[None, :]
+    p["rope"] = torch.cat([ang.cos(), ang.sin()], 1).to(torch.bfloat16).contiguous()
+    p["pos"] = torch.arange(ctx - M, ctx, dtype=torch.int32, device=dev)
+    p["slot"] = torch.arange(ctx - M, ctx, dtype=torch.int64, device=dev)
+    p["g_q"], p["g_kv"], p["ik_w"], p["ik_b"] = bf(2048), bf(512), bf(128), bf(128)
+    p["kv"] = torch.zeros(ctx, 576 * 2, dtype=torch.uint8, device=dev)
+    p["kv8"] = torch.zeros(ctx, 656, dtype=torch.uint8, device=dev)
+    p["idx"] = torch.zeros(ctx // 64 * 64 * 132, dtype=torch.uint8, device=dev)
+    p["qq"] = torch.empty(M, 2048, dtype=torch.uint8, device=dev)
+    p["qsf"] = torch.empty(4 * M * 4, dtype=torch.uint8, device=dev)
+    p["qmla"] = torch.empty(M, 64, 576, dtype=torch.bfloat16, device=dev)
+    p["iq"] = torch.empty(M, 32, 128, dtype=torch.uint8, device=dev)
+    p["iw"], p["wout"] = bf(M, 32), torch.empty(M, 32, dtype=torch.float32, device=dev)
+    x, qb = data["q_a_kv_a"]["c"], data["q_b"]["c"]
+    mla = lambda fp8: (lambda: ops.mla_prep(x, 2752, p["g_q"], p["g_kv"], p["rope"], p["pos"], p["slot"],
+                                            p["kv8" if fp8 else "kv"], p["idx"], p["ik_w"], p["ik_b"], p["qq"],
+                                            p["qsf"], M, M, fp8=fp8, num_slots=ctx, rope_rows=ctx))
+    return p, [
+        # read h, res; write res, xn, xq, xsf
+        ("add_rms_quant", lambda: ops.add_rms_quant(p["h"], p["res"], p["gamma"], p["xn"], p["xq"], p["xsf"], M, M),
+         M * (5 * 2 * H + H + H // 128)),
+        # read the 2752-wide row and its rope row; write qq, qsf, the cache row and the index row
+        ("mla_prep", mla(False), M * (2752 * 2 + 128 + 2048 + 16 + 1152 + 132)),
+        ("mla_prep_fp8", mla(True), M * (2752 * 2 + 128 + 2048 + 16 + 656 + 132)),
+        # read 64 q_pe, 32 indexer heads, iw and the rope row; write the q_pe tails, iq and wout
+        ("q_post", lambda: ops.q_post(qb, 20480, p["rope"], p["pos"], p["qmla"], p["iq"], p["iw"], p["wout"], 1, M,
+                                      rope_rows=ctx),
+         M * (64 * 128 + 32 * 256 + 64 + 128 + 64 * 128 + 32 * 128 + 128)),
+    ]
+
+
 def aux_prepare(data, dev):
     """Operands of the absorbed-MLA batched GEMMs and the indexer's MQA logits at the M = 16384 chunk of one
     65536-token sequence (scripts/gen.py:136-139, 178-179, 376, 382-387, 401)."""
@@ -346,6 +390,14 @@ def main():
         if nbytes:
             glue[name].update(gbps=round(nbytes / (ms * 1e-3) / 1e9, 1), frac_hbm=round(nbytes / (ms * 1e-3) / PEAK_HBM, 4))
     log("glue (us): " + ", ".join(f"{k} {v['us']}" for k, v in glue.items()))
+    producers = {}
+    pbufs, plaunch = producer_launches(data, dev)
+    for name, fn, nbytes in plaunch:
+        ms = time_launch(fn, stream)
+        producers[name] = {"us": round(ms * 1e3, 1), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                           "frac_hbm": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4)}
+    del pbufs
+    log("producers (us): " + ", ".join(f"{k} {v['us']} ({v['gbps']} GB/s)" for k, v in producers.items()))
     aux = {}
     aux_data = aux_prepare(data, dev)
     for name, fn, flops, nbytes, bound in aux_launches(aux_data):
@@ -375,6 +427,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": per,
         "glue": glue,
+        "producers": producers,
         "aux": aux,
     }
     print(json.dumps(line), flush=True)

@@ -83,6 +83,47 @@ int kg_quant(const void* x, int ldx, void* q, void* sf, int sf_rows, int K, int 
  * live rows.  The exp is this library's (kg_exp), not CUDA's __expf. */
 int kg_silu_mul_quant(const void* gu, int I, void* q, void* sf, int sf_rows, const int* n, int rows, void* stream);
 
+/* ---------------------------------------------------------------- operand producers (module glm_glue) */
+
+/* glm_add_rms_quant (source/glm_glue.cu:127-162; ops add_rms_quant, rms_quant (a NULL) and head_norm (q, sf
+ * NULL), scripts/gen.py:156-158, 167-171): rows of H = 6144 bf16.  res = bf16(res + a) (a NULL: res is only
+ * read), normed = bf16(bf16(res * rr) * gamma) with rr = 1 / sqrt(sum(res^2) / 6144 + 1e-5), and normed
+ * quantized per 128 columns into q [T][6144] and sf words [12][sf_rows] (eps 1e-10).  normed may be NULL, q
+ * and sf are NULL together.  The sum of squares follows the reference's thread / butterfly order; its
+ * rsqrtf is the correctly rounded 1 / sqrt here.  Requires res, gamma, a and normed 16-byte aligned, q
+ * 8-byte, sf 4-byte aligned, T <= sf_rows. */
+int kg_add_rms_quant(const void* a, void* res, const void* gamma, void* normed, void* q, void* sf, int sf_rows,
+                     int T, void* stream);
+
+/* glm_mla_prep (bf16 latent cache) and glm_mla_prep_fp8 (its fp8 row), source/glm_glue.cu:196-299; ops
+ * mla_prep_full / mla_prep_shared (idx, ik_w, ik_b NULL), scripts/gen.py:172-177, 369-374.  Row r of x (lda
+ * bf16 apart) is [q_a 2048 | kv_a 512 | k_pe 64 | wk 128]:
+ *   qq [T][2048] / qsf words [4][sf_rows] = per-128 quant (eps 1e-10) of bf16(q_a * rq * g_q);
+ *   kv row slot[r] (576 bf16 = 1152 bytes, or fp8: 512 e4m3 of kv / (amax_tile / 448) per 128-column tile,
+ *   4 f32 tile scales, 64 bf16 = 656 bytes) = bf16(kv_a * rk * g_kv) | rope(k_pe);
+ *   idx page slot / 64 (64 rows of 128 e4m3, then 64 f32 scales), row slot % 64 = e4m3 of rope(LayerNorm(wk)
+ *   * ik_w + ik_b) (eps 1e-6, rope on dims 0-63) with one UE8M0 scale (eps 1e-4).
+ * rope [rope_rows][64] bf16: 32 cos then 32 sin of position pos[r]; slot int64.  Cache rows are written only
+ * when 0 <= slot[r] < num_slots and 0 <= pos[r] < rope_rows (the reference checks slot >= 0; the two bounds
+ * are this ABI's, so that a bad slot or position cannot write outside the caches).  Requires lda % 8 == 0,
+ * lda >= 2624 (2752 with idx), T <= sf_rows, x, g_q, g_kv, kv, ik_w, ik_b 16-byte, qq, idx, rope 8-byte,
+ * qsf 4-byte aligned. */
+int kg_mla_prep(const void* x, int lda, const void* g_q, const void* g_kv, const void* rope, const int* pos,
+                const long long* slot, void* kv, void* idx, const void* ik_w, const void* ik_b, void* qq, void* qsf,
+                int sf_rows, int T, long long num_slots, int rope_rows, void* stream);
+int kg_mla_prep_fp8(const void* x, int lda, const void* g_q, const void* g_kv, const void* rope, const int* pos,
+                    const long long* slot, void* kv, void* idx, const void* ik_w, const void* ik_b, void* qq,
+                    void* qsf, int sf_rows, int T, long long num_slots, int rope_rows, void* stream);
+
+/* glm_q_post (source/glm_glue.cu:301-351; ops q_post_full / q_post_shared (iq, iw, wout NULL, full 0),
+ * scripts/gen.py:117-122, 378, 394): per row of qb (ldb bf16 apart, 64 heads of nope 192 | pe 64, then the
+ * indexer's 32 heads of 128 at column 16384), qmla [T][64][576] columns 512-575 of every head = rope(q_pe);
+ * with full, iq [T][32][128] = e4m3 of rope(q_idx) (dims 0-63 roped) per (row, head) with a UE8M0 scale sc
+ * (eps 1e-4), and wout [T][32] = ((f32(iw) * sc) * 128^-1/2) * 32^-1/2.  Rows with pos outside
+ * [0, rope_rows) are skipped.  Requires ldb % 8 == 0, qb and qmla 16-byte, iq and rope 8-byte aligned. */
+int kg_q_post(const void* qb, int ldb, const void* rope, const int* pos, void* qmla, void* iq, const void* iw,
+              float* wout, int full, int T, int rope_rows, void* stream);
+
 /* FlashInfer routingPrecomputed tables (the `routing(experts, topk, tile)` op, scripts/glm_ops.py:207-233;
  * three launches as there).  ids int32 [T][topk] -> counts [2*experts] (upper half zero), cta_batch /
  * cta_limit [ctas], num_non_exiting [1], total_padded [1], route_map [mcap], exp2perm [T][topk];

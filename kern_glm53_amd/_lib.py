@@ -31,6 +31,10 @@ SIGNATURES = {
     "kg_router_topk": [P, P, P, P, P, I, P],
     "kg_requant": [P, P, P, P, I, I, I, I, I, I, LL, P],
     "kg_kvb": [P, P, P, P, P],
+    "kg_add_rms_quant": [P, P, P, P, P, P, I, I, P],
+    "kg_mla_prep": [P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, LL, I, P],
+    "kg_mla_prep_fp8": [P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, LL, I, P],
+    "kg_q_post": [P, I, P, P, P, P, P, P, I, I, I, P],
 }
 
 _lib = None

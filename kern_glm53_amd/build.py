@@ -26,6 +26,7 @@ ARCH = "gfx950"
 SOURCES = {
     "kg_glue.hip": ["-ffp-contract=off"],
     "kg_prep.hip": ["-ffp-contract=off"],
+    "kg_norm_rope.hip": ["-ffp-contract=off"],
     "kg_fp8_gemm.hip": [],
     "kg_bf16_batched.hip": [],
     "kg_mqa_logits.hip": ["-fno-honor-nans"],

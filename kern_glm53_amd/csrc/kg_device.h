@@ -117,3 +117,17 @@ KG_DEV float kg_group_max(float v) {
   for (int o = WIDTH / 2; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// Max over each row of 16 lanes through DPP (a max does not depend on the pairing): quad permutes [1,0,3,2]
+// and [2,3,0,1], then the half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i).
+template <int CTRL>
+KG_DEV float kg_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+KG_DEV float kg_row16_max(float v) {
+  v = fmaxf(v, kg_dpp<0xb1>(v));
+  v = fmaxf(v, kg_dpp<0x4e>(v));
+  v = fmaxf(v, kg_dpp<0x141>(v));
+  v = fmaxf(v, kg_dpp<0x140>(v));
+  return v;
+}

@@ -16,6 +16,7 @@ from ._lib import call
 __all__ = [
     "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "bf16_batched", "mqa_logits", "quant",
     "silu_mul_quant", "routing", "moe_psum", "moe_gather", "moe_combine", "router_topk", "requant", "kvb",
+    "add_rms_quant", "mla_prep", "q_post",
     "sf_words", "counts_len", "EXPERTS", "TOPK", "TILE",
 ]
 
@@ -92,6 +93,26 @@ def quant(x, ldx: int, q, sf, sf_rows: int, K: int, T: int):
 def silu_mul_quant(gu, I: int, q, sf, sf_rows: int, n, rows: int):
     """glm_silu_mul_quant (source/glm_glue.cu:177-194); `n` is a device int tensor or None."""
     call("kg_silu_mul_quant", _ptr(gu), I, _ptr(q), _ptr(sf), sf_rows, _ptr(n), rows, _stream())
+
+
+def add_rms_quant(a, res, gamma, normed, q, sf, sf_rows: int, T: int):
+    """glm_add_rms_quant (source/glm_glue.cu:127-162): a None is the `rms_quant` op, q / sf None `head_norm`."""
+    call("kg_add_rms_quant", _ptr(a), _ptr(res), _ptr(gamma), _ptr(normed), _ptr(q), _ptr(sf), sf_rows, T, _stream())
+
+
+def mla_prep(x, lda: int, g_q, g_kv, rope, pos, slot, kv, idx, ik_w, ik_b, qq, qsf, sf_rows: int, T: int, *,
+             fp8: bool, num_slots: int, rope_rows: int):
+    """glm_mla_prep / glm_mla_prep_fp8 (source/glm_glue.cu:196-299); idx / ik_w / ik_b None is `mla_prep_shared`.
+    num_slots and rope_rows bound the cache rows and positions written."""
+    call("kg_mla_prep_fp8" if fp8 else "kg_mla_prep", _ptr(x), lda, _ptr(g_q), _ptr(g_kv), _ptr(rope), _ptr(pos),
+         _ptr(slot), _ptr(kv), _ptr(idx), _ptr(ik_w), _ptr(ik_b), _ptr(qq), _ptr(qsf), sf_rows, T, num_slots,
+         rope_rows, _stream())
+
+
+def q_post(qb, ldb: int, rope, pos, qmla, iq, iw, wout, full: int, T: int, *, rope_rows: int):
+    """glm_q_post (source/glm_glue.cu:301-351); full = 0 with iq / iw / wout None is `q_post_shared`."""
+    call("kg_q_post", _ptr(qb), ldb, _ptr(rope), _ptr(pos), _ptr(qmla), _ptr(iq), _ptr(iw), _ptr(wout), full, T,
+         rope_rows, _stream())
 
 
 def routing(ids, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, *, T: int,

@@ -308,6 +308,267 @@ void kgo_kvb(const u8* w, const float* s, u16* kvb, u16* wuk) {
   }
 }
 
+/* ---------------------------------------------------------------- operand producers (f1): RMSNorm, rope */
+
+#define KGO_QL 2048       /* q_a width: source/glm_glue.cu:27 */
+#define KGO_KVL 512       /* kv_a width: 28 */
+#define KGO_HALF 32       /* rope pairs: 29 */
+#define KGO_HEADS 64      /* attention heads: 30 */
+#define KGO_QHD 256       /* q head width (nope 192 | pe 64): 31-32 */
+#define KGO_NOPE 192
+#define KGO_MLA 576       /* latent cache row, bf16 elements: 33 */
+#define KGO_IH 32         /* indexer heads: 34 */
+#define KGO_ID 128        /* indexer head width: 35 */
+#define KGO_PAGE 64       /* rows of an index-cache page: 37 */
+#define KGO_IDX_PAGE (KGO_PAGE * (KGO_ID + 4))
+#define KGO_KV8 (KGO_KVL + 16 + 2 * 64)   /* fp8 latent row bytes: 39 */
+#define KGO_EPS 1e-5f     /* RMSNorm epsilon: 40 */
+
+static inline float rnd_bf16(float x) { return kgo_bf16_to_f32(kgo_f32_to_bf16(x)); }
+
+/* The reference's rsqrtf (a hardware approximation, up to 2 ulp from 1/sqrt on its GPUs) is restated
+ * as the correctly rounded quotient 1 / sqrtf(x): both sides of this build evaluate exactly that, and it
+ * is within 3 ulp of the reference's value. */
+static inline float rsqrt_rn(float x) { return 1.0f / sqrtf(x); }
+
+/* warp_sum, source/glm_glue.cu:45-50: the xor butterfly over 32 lanes, offsets 16, 8, 4, 2, 1, each lane
+ * adding its partner's value; every lane ends with the same total (addition commutes). */
+static float warp_sum32(const float* v) {
+  float x[32], y[32];
+  memcpy(x, v, sizeof x);
+  for (int o = 16; o; o >>= 1) {
+    for (int l = 0; l < 32; ++l) y[l] = x[l] + x[l ^ o];
+    memcpy(x, y, sizeof x);
+  }
+  return x[0];
+}
+
+/* block_sum, source/glm_glue.cu:57-65: every warp's butterfly total, then the butterfly over the eight
+ * warp totals with lanes 8-31 holding zero. */
+static float block_sum256(const float* v) {
+  float t[32] = {0};
+  for (int w = 0; w < 8; ++w) t[w] = warp_sum32(v + 32 * w);
+  return warp_sum32(t);
+}
+
+/* One rotation of an interleaved rope pair (source/glm_glue.cu:259-262, 325-326, 273-274, 333-334):
+ * (x1 c - x2 s, x2 c + x1 s), each with its first product fused, the multiply-add contraction nvcc
+ * forms for these expressions under its default -fmad=true. */
+static inline void rope_pair(float x1, float x2, float c, float s, float* o1, float* o2) {
+  *o1 = fmaf(x1, c, -(x2 * s));
+  *o2 = fmaf(x2, c, x1 * s);
+}
+
+/* glm_add_rms_quant, source/glm_glue.cu:127-162, rows of H = 6144: res = bf16(res + a) (a may be NULL:
+ * res is read as is and not written), normed = bf16(bf16(res * rr) * gamma) with rr = rsqrt(block_sum(ss)
+ * / H + 1e-5), and normed quantized per 128 columns into q / sf (eps 1e-10).  ss is thread t = 32 w + l's
+ * fused chain over its 24 values (blocks 6w .. 6w+5, columns 4l .. 4l+3 of each, in that order), summed
+ * by block_sum.  normed and q may be NULL. */
+/* rr of one 6144-wide row (its f32 values v) as glm_add_rms_quant forms it, source/glm_glue.cu:134-150. */
+float kgo_rms_rr6144(const float* v) {
+  float part[256];
+  for (int t = 0; t < 256; ++t) {
+    const int w = t >> 5, l = t & 31;
+    float ss = 0.0f;
+    for (int i = 0; i < 6; ++i)
+      for (int j = 0; j < 4; ++j) {
+        const float x = v[(w * 6 + i) * 128 + l * 4 + j];
+        ss = fmaf(x, x, ss);
+      }
+    part[t] = ss;
+  }
+  return rsqrt_rn(block_sum256(part) / (float)KGO_H + KGO_EPS);
+}
+
+void kgo_add_rms_quant(const u16* a, u16* res, const u16* gamma, u16* normed, u8* q, u8* sf, int sf_rows, int T) {
+  static float v[KGO_H];
+  float y[128];
+  for (int r = 0; r < T; ++r) {
+    u16* row = res + (size_t)r * KGO_H;
+    for (int c = 0; c < KGO_H; ++c) {
+      float x = kgo_bf16_to_f32(row[c]);
+      if (a) {
+        x = rnd_bf16(x + kgo_bf16_to_f32(a[(size_t)r * KGO_H + c]));
+        row[c] = kgo_f32_to_bf16(x);
+      }
+      v[c] = x;
+    }
+    const float rr = kgo_rms_rr6144(v);
+    for (int kb = 0; kb < KGO_H / 128; ++kb) {
+      for (int i = 0; i < 128; ++i) {
+        const int c = kb * 128 + i;
+        y[i] = rnd_bf16(rnd_bf16(v[c] * rr) * kgo_bf16_to_f32(gamma[c]));
+        if (normed) normed[(size_t)r * KGO_H + c] = kgo_f32_to_bf16(y[i]);
+      }
+      if (q) quant_block(y, q + (size_t)r * KGO_H + kb * 128, sf, sf_rows, r, kb, 1e-10f);
+    }
+  }
+}
+
+/* glm_mla_prep / glm_mla_prep_fp8, source/glm_glue.cu:196-299.  Row r of x (lda apart) is [q_a 2048 |
+ * kv_a 512 | k_pe 64 | wk 128]:
+ *   q_c = bf16(q_a * rq * g_q) quantized per 128 columns into qq [T][2048] / qsf (eps 1e-10), rq from
+ *     thread t's fused chain over blocks 2w, 2w+1 (columns 4l .. 4l+3 of each) and block_sum;
+ *   when 0 <= slot[r] < num_slots and 0 <= pos[r] < rope_rows (the reference checks only slot >= 0):
+ *     kv row slot[r] = bf16(kv_a * rk * g_kv) | rope(k_pe): either 576 bf16, or (fp8) 512 e4m3 codes of
+ *     kv / (amax_tile / 448) per 128-column tile, the 4 f32 tile scales, then the 64 bf16 of k_pe; rk from
+ *     thread t's kv_a[2t]^2 + kv_a[2t+1]^2 (the first product fused) and block_sum;
+ *     idx (may be NULL): k = rope(LayerNorm(wk)) (eps 1e-6, affine ik_w / ik_b, rope on dims 0-63), e4m3
+ *     with one UE8M0 scale (eps 1e-4), at row slot % 64 of page slot / 64 (64 rows of 128 bytes, then
+ *     the 64 f32 scales).
+ * The LayerNorm sums follow warp 7's lanes: mean = warp_sum(((k0 + k1) + k2) + k3) / 128, the variance a
+ * fused chain per lane then warp_sum.  rope [rope_rows][64] bf16: 32 cos, then 32 sin. */
+/* The four row statistics of mla_prep (source/glm_glue.cu:210-225, 265-272) for one row [q_a | kv_a |
+ * k_pe | wk]: st[0] = rq, st[1] = rk, st[2] = the wk LayerNorm's mean, st[3] its rstd. */
+static void mla_norm_stats(const u16* row, float* st) {
+  float part[256];
+  for (int t = 0; t < 256; ++t) {
+    const int w = t >> 5, l = t & 31;
+    float ss = 0.0f;
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 4; ++j) {
+        const float v = kgo_bf16_to_f32(row[(w * 2 + i) * 128 + l * 4 + j]);
+        ss = fmaf(v, v, ss);
+      }
+    part[t] = ss;
+  }
+  st[0] = rsqrt_rn(block_sum256(part) / (float)KGO_QL + KGO_EPS);
+  for (int t = 0; t < 256; ++t) {
+    const float k0 = kgo_bf16_to_f32(row[KGO_QL + 2 * t]), k1 = kgo_bf16_to_f32(row[KGO_QL + 2 * t + 1]);
+    part[t] = fmaf(k0, k0, k1 * k1);
+  }
+  st[1] = rsqrt_rn(block_sum256(part) / (float)KGO_KVL + KGO_EPS);
+}
+
+static void mla_ln_stats(const u16* row, float* st) {
+  float k[KGO_ID], ps[32];
+  const u16* wk = row + KGO_QL + KGO_KVL + 2 * KGO_HALF;
+  for (int c = 0; c < KGO_ID; ++c) k[c] = kgo_bf16_to_f32(wk[c]);
+  for (int l = 0; l < 32; ++l) ps[l] = ((k[4 * l] + k[4 * l + 1]) + k[4 * l + 2]) + k[4 * l + 3];
+  const float mean = warp_sum32(ps) / (float)KGO_ID;
+  for (int l = 0; l < 32; ++l) {
+    float d2 = 0.0f;
+    for (int j = 0; j < 4; ++j) d2 = fmaf(k[4 * l + j] - mean, k[4 * l + j] - mean, d2);
+    ps[l] = d2;
+  }
+  st[2] = mean;
+  st[3] = rsqrt_rn(warp_sum32(ps) / (float)KGO_ID + 1e-6f);
+}
+
+void kgo_mla_stats(const u16* row, float* st) {
+  mla_norm_stats(row, st);
+  mla_ln_stats(row, st);
+}
+
+void kgo_mla_prep(const u16* x, int lda, const u16* g_q, const u16* g_kv, const u16* rope, const int* pos,
+                  const long long* slot, u8* kv, u8* idx, const u16* ik_w, const u16* ik_b, u8* qq, u8* qsf,
+                  int sf_rows, int T, long long num_slots, int rope_rows, int fp8) {
+  float y[128], kvn[KGO_KVL], st[4];
+  for (int r = 0; r < T; ++r) {
+    const u16* row = x + (size_t)r * lda;
+    mla_norm_stats(row, st);
+    if (idx) mla_ln_stats(row, st);          /* the wk columns exist only on rows of indexer layers */
+    const float rq = st[0], rk = st[1];
+    for (int kb = 0; kb < KGO_QL / 128; ++kb) {
+      for (int i = 0; i < 128; ++i) {
+        const int c = kb * 128 + i;
+        y[i] = rnd_bf16(kgo_bf16_to_f32(row[c]) * rq * kgo_bf16_to_f32(g_q[c]));
+      }
+      quant_block(y, qq + (size_t)r * KGO_QL + kb * 128, qsf, sf_rows, r, kb, 1e-10f);
+    }
+    const long long s = slot[r];
+    const int p = pos[r];
+    if (s < 0 || s >= num_slots || p < 0 || p >= rope_rows) continue;
+    const u16* cs = rope + (size_t)p * 2 * KGO_HALF;
+    for (int c = 0; c < KGO_KVL; ++c)
+      kvn[c] = rnd_bf16(kgo_bf16_to_f32(row[KGO_QL + c]) * rk * kgo_bf16_to_f32(g_kv[c]));
+    u8* dst = kv + s * (fp8 ? KGO_KV8 : KGO_MLA * 2);
+    u8* pe = dst + (fp8 ? KGO_KVL + 16 : KGO_KVL * 2);
+    if (fp8) {
+      for (int tile = 0; tile < 4; ++tile) {
+        float amax = 0.0f;
+        for (int i = 0; i < 128; ++i) amax = fmaxf(amax, fabsf(kvn[tile * 128 + i]));
+        const float sc = amax / 448.0f, inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+        for (int i = 0; i < 128; ++i) dst[tile * 128 + i] = kgo_e4m3_from_f32(kvn[tile * 128 + i] * inv);
+        memcpy(dst + KGO_KVL + 4 * tile, &sc, 4);
+      }
+    } else {
+      for (int c = 0; c < KGO_KVL; ++c) {
+        const u16 h = kgo_f32_to_bf16(kvn[c]);
+        memcpy(dst + 2 * c, &h, 2);
+      }
+    }
+    for (int t = 0; t < KGO_HALF; ++t) {
+      const float x1 = kgo_bf16_to_f32(row[KGO_QL + KGO_KVL + 2 * t]);
+      const float x2 = kgo_bf16_to_f32(row[KGO_QL + KGO_KVL + 2 * t + 1]);
+      float o1, o2;
+      rope_pair(x1, x2, kgo_bf16_to_f32(cs[t]), kgo_bf16_to_f32(cs[KGO_HALF + t]), &o1, &o2);
+      const u16 h1 = kgo_f32_to_bf16(o1), h2 = kgo_f32_to_bf16(o2);
+      memcpy(pe + 4 * t, &h1, 2);
+      memcpy(pe + 4 * t + 2, &h2, 2);
+    }
+    if (!idx) continue;
+    const u16* wk = row + KGO_QL + KGO_KVL + 2 * KGO_HALF;
+    const float mean = st[2], rstd = st[3];
+    float k[KGO_ID], n[KGO_ID];
+    for (int c = 0; c < KGO_ID; ++c) k[c] = kgo_bf16_to_f32(wk[c]);
+    for (int c = 0; c < KGO_ID; ++c)
+      n[c] = fmaf((k[c] - mean) * rstd, kgo_bf16_to_f32(ik_w[c]), kgo_bf16_to_f32(ik_b[c]));
+    for (int pr = 0; pr < KGO_HALF; ++pr)
+      rope_pair(n[2 * pr], n[2 * pr + 1], kgo_bf16_to_f32(cs[pr]), kgo_bf16_to_f32(cs[KGO_HALF + pr]), &n[2 * pr],
+                &n[2 * pr + 1]);
+    float amax = 0.0f, sc;
+    for (int c = 0; c < KGO_ID; ++c) amax = fmaxf(amax, fabsf(n[c]));
+    kgo_ue8m0(amax, 1e-4f, &sc);
+    u8* page = idx + (size_t)(s / KGO_PAGE) * KGO_IDX_PAGE;
+    const int i = (int)(s % KGO_PAGE);
+    for (int c = 0; c < KGO_ID; ++c) page[i * KGO_ID + c] = kgo_e4m3_from_f32(n[c] / sc);
+    memcpy(page + KGO_PAGE * KGO_ID + 4 * i, &sc, 4);
+  }
+}
+
+/* glm_q_post, source/glm_glue.cu:301-351: per row of qb (ldb apart), the rope of every head's q_pe
+ * (columns h*256 + 192 .. +64) into columns 512 .. 576 of qmla [T][64][576]; with `full`, the indexer
+ * query (32 heads of 128 at column 16384) roped on its first 64 dims, quantized per (row, head) with a
+ * UE8M0 scale (eps 1e-4) into iq [T][32][128], and wout = ((f32(iw) * scale) * 128^-1/2) * 32^-1/2.  Rows
+ * with pos outside [0, rope_rows) are skipped (the reference does not check). */
+void kgo_q_post(const u16* qb, int ldb, const u16* rope, const int* pos, u16* qmla, u8* iq, const u16* iw,
+                float* wout, int full, int T, int rope_rows) {
+  float v[KGO_ID];
+  for (int r = 0; r < T; ++r) {
+    const int p = pos[r];
+    if (p < 0 || p >= rope_rows) continue;
+    const u16* row = qb + (size_t)r * ldb;
+    const u16* cs = rope + (size_t)p * 2 * KGO_HALF;
+    for (int h = 0; h < KGO_HEADS; ++h)
+      for (int pr = 0; pr < KGO_HALF; ++pr) {
+        const float x1 = kgo_bf16_to_f32(row[h * KGO_QHD + KGO_NOPE + 2 * pr]);
+        const float x2 = kgo_bf16_to_f32(row[h * KGO_QHD + KGO_NOPE + 2 * pr + 1]);
+        float o1, o2;
+        rope_pair(x1, x2, kgo_bf16_to_f32(cs[pr]), kgo_bf16_to_f32(cs[KGO_HALF + pr]), &o1, &o2);
+        u16* d = qmla + ((size_t)r * KGO_HEADS + h) * KGO_MLA + KGO_KVL + 2 * pr;
+        d[0] = kgo_f32_to_bf16(o1);
+        d[1] = kgo_f32_to_bf16(o2);
+      }
+    if (!full) continue;
+    for (int ih = 0; ih < KGO_IH; ++ih) {
+      for (int c = 0; c < KGO_ID; ++c) v[c] = kgo_bf16_to_f32(row[KGO_HEADS * KGO_QHD + ih * KGO_ID + c]);
+      for (int pr = 0; pr < KGO_HALF; ++pr)
+        rope_pair(v[2 * pr], v[2 * pr + 1], kgo_bf16_to_f32(cs[pr]), kgo_bf16_to_f32(cs[KGO_HALF + pr]),
+                  &v[2 * pr], &v[2 * pr + 1]);
+      float amax = 0.0f, sc;
+      for (int c = 0; c < KGO_ID; ++c) amax = fmaxf(amax, fabsf(v[c]));
+      kgo_ue8m0(amax, 1e-4f, &sc);
+      for (int c = 0; c < KGO_ID; ++c) iq[((size_t)r * KGO_IH + ih) * KGO_ID + c] = kgo_e4m3_from_f32(v[c] / sc);
+      float w = kgo_bf16_to_f32(iw[(size_t)r * KGO_IH + ih]);
+      w *= sc;
+      w *= 0.08838834764831845f;
+      w *= 0.17677669529663687f;
+      wout[(size_t)r * KGO_IH + ih] = w;
+    }
+  }
+}
+
 /* ---------------------------------------------------------------- array helpers for the Python side */
 
 void kgo_e4m3_encode_n(const float* x, u8* q, long long n) {

@@ -202,6 +202,75 @@ def router_topk(S: np.ndarray, bias: np.ndarray, rs_bf16: int):
     return idx, wts
 
 
+# ------------------------------------------------------------------ operand producers (f1)
+
+KV_ROW_BF16, KV_ROW_FP8, IDX_PAGE = 576 * 2, 512 + 16 + 128, 64 * 132   # source/glm_glue.cu:33, 36-39
+
+
+def add_rms_quant(a, res, gamma, sf_rows: int, normed=True, quant=True, q=None, sf=None):
+    """glm_add_rms_quant (source/glm_glue.cu:127-162) over rows of 6144.  a (or None) and res are bf16 bits
+    [T][6144]; res is updated in place when a is given.  Returns (normed or None, q or None, sf or None)."""
+    res_ = res
+    assert res_.flags["C_CONTIGUOUS"] and res_.dtype == np.uint16
+    T = res_.shape[0]
+    a_ = None if a is None else np.ascontiguousarray(a, dtype=np.uint16)
+    g = np.ascontiguousarray(gamma, dtype=np.uint16)
+    nrm = np.zeros((T, 6144), dtype=np.uint16) if normed else None
+    if quant:
+        q = np.zeros((T, 6144), dtype=np.uint8) if q is None else q
+        sf = np.zeros(sf_words(6144) * sf_rows * 4, dtype=np.uint8) if sf is None else sf
+    else:
+        q = sf = None
+    lib().kgo_add_rms_quant(None if a_ is None else _p(a_), _p(res_), _p(g), None if nrm is None else _p(nrm),
+                            None if q is None else _p(q), None if sf is None else _p(sf), ctypes.c_int(sf_rows),
+                            ctypes.c_int(T))
+    return nrm, q, sf
+
+
+def rms_rr6144(v) -> np.ndarray:
+    """rr of each 6144-wide row of f32 values v as glm_add_rms_quant forms it (source/glm_glue.cu:134-150)."""
+    v = np.ascontiguousarray(np.atleast_2d(v), dtype=np.float32)
+    lib().kgo_rms_rr6144.restype = ctypes.c_float
+    return np.array([lib().kgo_rms_rr6144(_p(row)) for row in v], dtype=np.float32)
+
+
+def mla_stats(x) -> np.ndarray:
+    """(rq, rk, mean, rstd) of each row [q_a | kv_a | k_pe | wk] (bf16 bits) as mla_prep forms them."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.uint16)
+    out = np.empty((x.shape[0], 4), dtype=np.float32)
+    for r in range(x.shape[0]):
+        lib().kgo_mla_stats(_p(x[r]), _p(out[r]))
+    return out
+
+
+def mla_prep(x, g_q, g_kv, rope, pos, slot, kv, idx, ik_w, ik_b, qq, qsf, sf_rows: int, T: int, fp8: bool):
+    """glm_mla_prep / glm_mla_prep_fp8 (source/glm_glue.cu:196-299), writing kv / idx / qq / qsf in place.
+    x bf16 bits [T][lda]; kv uint8 [num_slots][576*2 or 656]; idx uint8 pages or None."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    arrs = [np.ascontiguousarray(v, dtype=np.uint16) for v in (g_q, g_kv, rope)]
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    slot = np.ascontiguousarray(slot, dtype=np.int64)
+    kw = None if ik_w is None else np.ascontiguousarray(ik_w, dtype=np.uint16)
+    kb = None if ik_b is None else np.ascontiguousarray(ik_b, dtype=np.uint16)
+    num_slots = kv.shape[0]
+    lib().kgo_mla_prep(_p(x), ctypes.c_int(x.shape[1]), _p(arrs[0]), _p(arrs[1]), _p(arrs[2]), _p(pos), _p(slot),
+                       _p(kv), None if idx is None else _p(idx), None if kw is None else _p(kw),
+                       None if kb is None else _p(kb), _p(qq), _p(qsf), ctypes.c_int(sf_rows), ctypes.c_int(T),
+                       ctypes.c_longlong(num_slots), ctypes.c_int(arrs[2].shape[0]), ctypes.c_int(1 if fp8 else 0))
+
+
+def q_post(qb, rope, pos, qmla, iq, iw, wout, full: bool, T: int):
+    """glm_q_post (source/glm_glue.cu:301-351), writing qmla (bf16 bits [T][64][576], columns 512-575 of each
+    head), iq [T][32][128] and wout [T][32] in place."""
+    qb = np.ascontiguousarray(qb, dtype=np.uint16)
+    rope = np.ascontiguousarray(rope, dtype=np.uint16)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    iw_ = None if iw is None else np.ascontiguousarray(iw, dtype=np.uint16)
+    lib().kgo_q_post(_p(qb), ctypes.c_int(qb.shape[1]), _p(rope), _p(pos), _p(qmla), None if iq is None else _p(iq),
+                     None if iw_ is None else _p(iw_), None if wout is None else _p(wout), ctypes.c_int(int(full)),
+                     ctypes.c_int(T), ctypes.c_int(rope.shape[0]))
+
+
 # ------------------------------------------------------------------ weight layout (a12, a13)
 
 def requant(w8, s, wq, sf, rows, K, group_rows, dst_group_rows=0, dst_row0=0, sf_ld=None, sf_group=0):

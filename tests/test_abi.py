@@ -48,6 +48,10 @@ NULL = None
     ("kg_quant", [NULL, 128, NULL, NULL, 16, 128, 16, NULL]),
     ("kg_moe_psum", [NULL, NULL, NULL]),
     ("kg_kvb", [NULL, NULL, NULL, NULL, NULL]),
+    ("kg_add_rms_quant", [NULL, NULL, NULL, NULL, NULL, NULL, 16, 16, NULL]),
+    ("kg_mla_prep", [NULL, 2752, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 16, 16, 64, 64,
+                     NULL]),
+    ("kg_q_post", [NULL, 20480, NULL, NULL, NULL, NULL, NULL, NULL, 1, 16, 64, NULL]),
 ])
 def test_null_pointers_rejected(name, args):
     assert getattr(_lib.lib(), name)(*args) == 1
@@ -89,6 +93,19 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     ("kg_requant", [FAKE, FAKE, FAKE, FAKE, 256, 128, 100, 0, 0, 256, 0, NULL]),
     # mqa: negative sizes
     ("kg_mqa_logits", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, 16, 256, NULL]),
+    # add_rms_quant: T > sf_rows, q without sf
+    ("kg_add_rms_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 17, NULL]),
+    ("kg_add_rms_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 16, 16, NULL]),
+    # mla_prep: lda too short for the indexer key, lda % 8, T > sf_rows
+    ("kg_mla_prep", [FAKE, 2624, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 16, 64, 64,
+                     NULL]),
+    ("kg_mla_prep_fp8", [FAKE, 2756, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, NULL, NULL, FAKE, FAKE, 16, 16, 64, 64,
+                         NULL]),
+    ("kg_mla_prep", [FAKE, 2752, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL, NULL, NULL, FAKE, FAKE, 16, 17, 64, 64,
+                     NULL]),
+    # q_post: ldb too short for the indexer heads, full without iq
+    ("kg_q_post", [FAKE, 16384, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 16, 64, NULL]),
+    ("kg_q_post", [FAKE, 20480, FAKE, FAKE, FAKE, NULL, FAKE, FAKE, 1, 16, 64, NULL]),
 ])
 def test_invalid_shapes_rejected(name, args):
     assert getattr(_lib.lib(), name)(*args) == 1
