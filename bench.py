@@ -216,7 +216,7 @@ def producer_launches(data, dev):
     return p, [
         # read h, res; write res, xn, xq, xsf
         ("add_rms_quant", lambda: ops.add_rms_quant(p["h"], p["res"], p["gamma"], p["xn"], p["xq"], p["xsf"], M, M),
-         M * (5 * 2 * H + H + H // 128)),
+         M * (4 * 2 * H + H + H // 128)),
         # read the 2752-wide row and its rope row; write qq, qsf, the cache row and the index row
         ("mla_prep", mla(False), M * (2752 * 2 + 128 + 2048 + 16 + 1152 + 132)),
         ("mla_prep_fp8", mla(True), M * (2752 * 2 + 128 + 2048 + 16 + 656 + 132)),
