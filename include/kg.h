@@ -124,6 +124,41 @@ int kg_mla_prep_fp8(const void* x, int lda, const void* g_q, const void* g_kv, c
 int kg_q_post(const void* qb, int ldb, const void* rope, const int* pos, void* qmla, void* iq, const void* iw,
               float* wout, int full, int T, int rope_rows, void* stream);
 
+/* ---------------------------------------------------------------- indexer consumers (modules vllm_topk, glm_glue) */
+
+/* vLLM's prefill top-k over the MQA logits' compressed rows: the `glm_topk_prefill` launch of the
+ * `indexer(j, r, kv_cap)` op (scripts/glm_ops.py:123-127; source/vllm-topk/topk.cu:18-35 over
+ * sampler_topk.cuh:297-547).  For rows r = offset + i, i < num_rows (the reference's grid), of logits
+ * (stride0 floats apart), elements [starts[r], ends[r]): out[r][0:topk] = the topk indices (relative to
+ * starts[r]) of the largest values, ascending, ties at the threshold toward the smallest index (the
+ * reference lists the same set, up to its ties, in its atomics' order); a row of at most topk elements
+ * gives 0 .. len-1 then -1.  Requires stride1 == 1 (the op's), stride0 % 4 == 0, logits 16-byte aligned,
+ * topk <= 8192, and every row inside its stride0 floats. */
+int kg_topk_prefill(const float* logits, const int* starts, const int* ends, int* out, int num_rows, int stride0,
+                    int stride1, int topk, int offset, void* stream);
+
+/* glm_topk_stream (source/glm_glue.cu:416-427; op topk_stream, scripts/gen.py:130-132): ind [T][2048] in
+ * place, k -> ks[r] + k (-1 kept); tlen[r] = min(klen[r], 2048).  Requires ind 16-byte aligned. */
+int kg_topk_stream(int* ind, const unsigned* ks, const int* klen, int* tlen, int T, void* stream);
+
+/* glm_topk_slots (source/glm_glue.cu:429-444; op topk_slots, scripts/gen.py:127-129): ind [T][2048] in place,
+ * k -> block_table[row_seq[r]][k / 64] * 64 + k % 64 (-1 kept); tlen[r] = min(klen[r], 2048). */
+int kg_topk_slots(int* ind, const int* block_table, int max_pages, const int* row_seq, const int* klen, int* tlen,
+                  int T, void* stream);
+
+/* glm_idx_gather (source/glm_glue.cu:353-376; op idx_gather, scripts/gen.py:124-126): page j of sequence s of
+ * the paged index cache (64 rows of 128 e4m3, then 64 f32 scales, page block_table[s][j]) to stream rows
+ * goff(s) + 64 j of kg [.][128] and ksf, goff(s) = sum of the earlier seq_lens.  `blocks` is the reference's
+ * grid, ceil(ctx / 64) + nseq (blocks past the last page do nothing). */
+int kg_idx_gather(const void* idx, const int* block_table, int max_pages, const int* seq_lens, int nseq, void* kg,
+                  float* ksf, int blocks, void* stream);
+
+/* glm_kv_dequant (source/glm_glue.cu:378-414; op kv_dequant, scripts/gen.py:133-135): the fp8 latent rows
+ * (656 bytes: 512 e4m3, 4 f32 tile scales, 64 bf16) of each sequence's pages to bf16 [576] rows of the same
+ * stream, value bf16(f32(e4m3) * tile scale), k_pe copied.  `blocks` as kg_idx_gather's. */
+int kg_kv_dequant(const void* kv, const int* block_table, int max_pages, const int* seq_lens, int nseq, void* kvd,
+                  int blocks, void* stream);
+
 /* FlashInfer routingPrecomputed tables (the `routing(experts, topk, tile)` op, scripts/glm_ops.py:207-233;
  * three launches as there).  ids int32 [T][topk] -> counts [2*experts] (upper half zero), cta_batch /
  * cta_limit [ctas], num_non_exiting [1], total_padded [1], route_map [mcap], exp2perm [T][topk];

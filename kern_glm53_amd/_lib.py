@@ -35,6 +35,11 @@ SIGNATURES = {
     "kg_mla_prep": [P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, LL, I, P],
     "kg_mla_prep_fp8": [P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, LL, I, P],
     "kg_q_post": [P, I, P, P, P, P, P, P, I, I, I, P],
+    "kg_topk_prefill": [P, P, P, P, I, I, I, I, I, P],
+    "kg_topk_stream": [P, P, P, P, I, P],
+    "kg_topk_slots": [P, P, I, P, P, P, I, P],
+    "kg_idx_gather": [P, P, I, P, I, P, P, I, P],
+    "kg_kv_dequant": [P, P, I, P, I, P, I, P],
 }
 
 _lib = None

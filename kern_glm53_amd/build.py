@@ -27,6 +27,7 @@ SOURCES = {
     "kg_glue.hip": ["-ffp-contract=off"],
     "kg_prep.hip": ["-ffp-contract=off"],
     "kg_norm_rope.hip": ["-ffp-contract=off"],
+    "kg_indexer.hip": ["-ffp-contract=off"],
     "kg_fp8_gemm.hip": [],
     "kg_bf16_batched.hip": [],
     "kg_mqa_logits.hip": ["-fno-honor-nans"],

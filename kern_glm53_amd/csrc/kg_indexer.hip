@@ -1,0 +1,359 @@
+// The indexer's consumers on gfx950: the prefill top-k over the MQA logits' compressed rows (vLLM's
+// top_k_per_row_prefill behind glm_topk_prefill, source/vllm-topk/topk.cu:18-35, sampler_topk.cuh:297-547),
+// the maps of its indices to the attention's key rows (glm_topk_stream / glm_topk_slots,
+// source/glm_glue.cu:416-444), and the paged caches' gathers into per-chunk streams (glm_idx_gather,
+// glm_kv_dequant, 353-414).
+#include "kg_device.h"
+#include "kg_host.h"
+
+#define KG_TOPK 2048        // the attention's key budget: source/glm_glue.cu:36
+#define KG_PAGE 64
+#define KG_ID 128
+#define KG_IDX_PAGE (KG_PAGE * (KG_ID + 4))
+#define KG_KVL 512
+#define KG_MLA 576
+#define KG_KV8 (KG_KVL + 16 + 2 * 64)
+
+// ============================================================================ top-k
+
+// One 1024-thread workgroup per row.  A row of up to 65536 logits is read once into registers: thread t
+// holds elements [64 t, 64 t + 64) of a segment, so thread order is index order.  Longer rows are
+// processed in segments of 65536, re-read from memory on each pass.
+//
+// Selection is a radix select over the order-preserving key of the f32 bits (larger float, larger key;
+// -0 below +0, as the reference's bit transform orders them).  Valid keys are clamped to at least 1 (only a
+// NaN pattern maps to 0) and padding elements get key 0: they sort below every valid element, so they are
+// never taken and never move the threshold, and no pass tests validity.  The bits below the common prefix
+// of the row's smallest and largest valid keys are resolved at most 11 at a time: each pass histograms the
+// candidates' next bits (four interleaved copies, lane & 3, spreading a hot bin's atomics over four banks;
+// non-candidates add to a per-lane dummy slot, so the loop has no branches), then a block-wide suffix scan
+// finds the bin holding the K-th largest.  A pass ends the search early when that bin's elements are exactly
+// the ones still needed.  Output: the K selected indices (relative to the row start) in ascending order,
+// ties at the threshold broken toward the smallest index, staged in LDS and stored coalesced; rows of at
+// most K elements give 0 .. len-1 then -1 (the reference's shortcut).  The reference emits the same set up
+// to its ties, in the order its atomics happen to produce.
+#define KG_TK_T 1024
+#define KG_TK_V 64
+#define KG_TK_SEG (KG_TK_T * KG_TK_V)
+#define KG_TK_LDS 8192                 // histogram copies (4 x 2048), reused as the output staging area
+
+KG_DEV u32 kg_okey(float f) {
+  const u32 b = kg_f2u(f);
+  return max((b & 0x80000000u) ? ~b : (b | 0x80000000u), 1u);
+}
+
+// Exclusive scan over the block's 1024 threads; tot gets the total.  Two barriers (the second frees wsum).
+KG_DEV int kg_tk_scan(int v, int* wsum, int& tot) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int x = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += x;
+  }
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int base = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < KG_TK_T / 64; ++i) {
+    const int s = wsum[i];
+    base += i < w ? s : 0;
+    all += s;
+  }
+  __syncthreads();
+  tot = all;
+  return base + inc - v;
+}
+
+// MULTI = false: the row (end - start <= stride0 <= 65536) is held in registers; true: segments of 65536 are
+// re-read on every pass (stride0 > 65536).
+template <bool MULTI>
+__global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restrict__ logits,
+                                                           const int* __restrict__ starts,
+                                                           const int* __restrict__ ends, int* __restrict__ out,
+                                                           int stride0, int topk, int offset) {
+  __shared__ __attribute__((aligned(16))) int lds[KG_TK_LDS + 64];   // + a dummy slot per lane
+  __shared__ int wsum[KG_TK_T / 64];
+  __shared__ u32 red[2][KG_TK_T / 64];
+  __shared__ int found[3];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int r = blockIdx.x + offset;
+  const int start = starts[r], len = max(ends[r] - start, 0);
+  int* const orow = out + (size_t)r * topk;
+  if (len <= topk) {                           // the whole row, then -1
+    for (int i = t; i < topk; i += KG_TK_T) orow[i] = i < len ? i : -1;
+    return;
+  }
+  // Loads are 16-byte buffer loads from the 16-byte aligned origin a0 <= start (logits is 16-byte aligned
+  // and stride0 % 4 == 0) through a resource covering the valid part of the row, so a vector past it reads
+  // zeros; element i of the aligned row is valid for lo <= i < hi.  (A buffer load is one instruction the
+  // compiler cannot split into conditional scalar loads.)
+  const int a0 = start & ~3, lo = start - a0, hi = MULTI ? ends[r] - a0 : min(ends[r] - a0, KG_TK_SEG);
+  const __amdgpu_buffer_rsrc_t rrow =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(logits + (size_t)r * stride0 + a0), (short)0, hi * 4,
+                                        0x00020000);
+  const int nseg = MULTI ? (hi + KG_TK_SEG - 1) / KG_TK_SEG : 1;
+  u32 key[KG_TK_V];
+  auto load = [&](int seg) {
+    const int e0 = seg * KG_TK_SEG + t * KG_TK_V;
+#pragma unroll
+    for (int i = 0; i < KG_TK_V / 4; ++i) {
+      const auto f = __builtin_amdgcn_raw_buffer_load_b128(rrow, (unsigned)(e0 + 4 * i) * 4u, 0, 0);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32 k = kg_okey(kg_u2f(f[c]));
+        key[4 * i + c] = (unsigned)(e0 + 4 * i + c - lo) < (unsigned)(hi - lo) ? k : 0u;   // lo <= e < hi
+      }
+    }
+  };
+  if (!MULTI) load(0);
+
+  // smallest and largest valid key: the bits above their first difference are common to every candidate
+  u32 kmin = 0xffffffffu, kmax = 0u;
+  for (int seg = 0; seg < nseg; ++seg) {
+    if (MULTI) load(seg);
+#pragma unroll
+    for (int j = 0; j < KG_TK_V; ++j) kmin = min(kmin, key[j] ? key[j] : 0xffffffffu), kmax = max(kmax, key[j]);
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    kmin = min(kmin, (u32)__shfl_xor((int)kmin, o, 64));
+    kmax = max(kmax, (u32)__shfl_xor((int)kmax, o, 64));
+  }
+  if (lane == 0) red[0][w] = kmin, red[1][w] = kmax;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < KG_TK_T / 64; ++i) kmin = min(kmin, red[0][i]), kmax = max(kmax, red[1][i]);
+  const u32 diff = kmin ^ kmax;
+  int s = diff ? 32 - __builtin_clz(diff) : 0;   // low bits still to resolve
+  u32 m = s >= 32 ? 0u : (0xffffffffu << s);      // the resolved bits
+  u32 pm = kmax & m;                              // the threshold's resolved bits
+  int need = topk;                                // elements still to take among the candidates
+
+  while (s > 0) {
+    const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
+    for (int i = t; i < 4 * NB; i += KG_TK_T) lds[i] = 0;
+    __syncthreads();
+    for (int seg = 0; seg < nseg; ++seg) {
+      if (MULTI) load(seg);
+#pragma unroll
+      for (int j = 0; j < KG_TK_V; ++j) {
+        const int slot = (key[j] & m) == pm ? (int)((((key[j] >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
+                                            : KG_TK_LDS + lane;
+        __hip_atomic_fetch_add(&lds[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
+    __syncthreads();
+    // descending bins: thread t sums bins NB-1-2t and NB-2-2t (NB is even)
+    int hh = 0, hl = 0;
+    if (2 * t < NB) {
+      const int4 a = *reinterpret_cast<const int4*>(&lds[(NB - 1 - 2 * t) << 2]);
+      const int4 b = *reinterpret_cast<const int4*>(&lds[(NB - 2 - 2 * t) << 2]);
+      hh = (a.x + a.y) + (a.z + a.w);
+      hl = (b.x + b.y) + (b.z + b.w);
+    }
+    int tot;
+    const int above = kg_tk_scan(hh + hl, wsum, tot);
+    if (2 * t < NB) {
+      if (above < need && need <= above + hh) found[0] = NB - 1 - 2 * t, found[1] = above, found[2] = hh;
+      else if (above + hh < need && need <= above + hh + hl) found[0] = NB - 2 - 2 * t, found[1] = above + hh, found[2] = hl;
+    }
+    __syncthreads();
+    const int b = found[0], ab = found[1], cnt = found[2];
+    __syncthreads();
+    need -= ab;
+    pm |= (u32)b << s2;
+    m = 0xffffffffu << s2;
+    s = s2;
+    if (cnt == need) break;                       // uniform: every element of the bin is taken
+  }
+
+  // Output in index order: an element above the threshold's bits is taken; one equal to them is taken while
+  // fewer than `need` equal ones precede it.  Its position = taken elements of smaller index.  Indices go to
+  // their positions in LDS (the others to a dummy slot), then out coalesced.
+  int above_base = 0, eq_base = 0;
+  for (int seg = 0; seg < nseg; ++seg) {
+    if (MULTI) load(seg);
+    int na = 0, ne = 0;
+#pragma unroll
+    for (int j = 0; j < KG_TK_V; ++j) {
+      na += (key[j] & m) > pm ? 1 : 0;
+      ne += (key[j] & m) == pm ? 1 : 0;
+    }
+    int ta, te;
+    const int pa = kg_tk_scan(na, wsum, ta) + above_base;
+    int pe = kg_tk_scan(ne, wsum, te) + eq_base;
+    int pos = pa + min(pe, need);
+    const int e0 = seg * KG_TK_SEG + t * KG_TK_V - lo;     // indices relative to the row start
+#pragma unroll
+    for (int j = 0; j < KG_TK_V; ++j) {
+      const u32 kk = key[j] & m;
+      const bool take = kk > pm || (kk == pm && pe < need);
+      pe += kk == pm ? 1 : 0;
+      lds[take ? pos : KG_TK_LDS + lane] = e0 + j;
+      pos += take ? 1 : 0;
+    }
+    above_base += ta;
+    eq_base += te;
+  }
+  __syncthreads();
+  for (int i = t; i < topk; i += KG_TK_T) orow[i] = lds[i];
+}
+
+extern "C" int kg_topk_prefill(const float* logits, const int* starts, const int* ends, int* out, int num_rows,
+                               int stride0, int stride1, int topk, int offset, void* stream) {
+  KG_CHECK(logits && starts && ends && out && num_rows >= 0 && offset >= 0 && topk >= 1 && topk <= KG_TK_LDS &&
+           stride1 == 1);
+  KG_CHECK(stride0 >= 0 && stride0 % 4 == 0 && kg_aligned(logits, 16));
+  if (num_rows == 0) return 0;
+  if (stride0 <= KG_TK_SEG)
+    hipLaunchKernelGGL(kg_topk_kernel<false>, dim3(num_rows), dim3(KG_TK_T), 0, (hipStream_t)stream, logits, starts,
+                       ends, out, stride0, topk, offset);
+  else
+    hipLaunchKernelGGL(kg_topk_kernel<true>, dim3(num_rows), dim3(KG_TK_T), 0, (hipStream_t)stream, logits, starts,
+                       ends, out, stride0, topk, offset);
+  return (int)hipGetLastError();
+}
+
+// ============================================================================ index maps
+
+// glm_topk_stream (source/glm_glue.cu:416-427): sequence-relative key k -> stream row ks[r] + k (-1 stays),
+// tlen[r] = min(klen[r], 2048).  A wave per row, 32 indices (two 16-byte vectors) per lane.
+__global__ __launch_bounds__(256) void kg_topk_stream_kernel(int* __restrict__ ind, const unsigned* __restrict__ ks,
+                                                             const int* __restrict__ klen, int* __restrict__ tlen,
+                                                             int T) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= T) return;
+  const int add = (int)ks[r];
+  int4* row = reinterpret_cast<int4*>(ind + (size_t)r * KG_TOPK);
+#pragma unroll
+  for (int i = 0; i < KG_TOPK / 4 / 64; ++i) {
+    int4 v = row[i * 64 + lane];
+    v.x = v.x < 0 ? -1 : v.x + add;
+    v.y = v.y < 0 ? -1 : v.y + add;
+    v.z = v.z < 0 ? -1 : v.z + add;
+    v.w = v.w < 0 ? -1 : v.w + add;
+    row[i * 64 + lane] = v;
+  }
+  if (lane == 0) tlen[r] = min(klen[r], KG_TOPK);
+}
+
+extern "C" int kg_topk_stream(int* ind, const unsigned* ks, const int* klen, int* tlen, int T, void* stream) {
+  KG_CHECK(ind && ks && klen && tlen && T >= 0 && kg_aligned(ind, 16));
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(kg_topk_stream_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, ind, ks, klen, tlen,
+                     T);
+  return (int)hipGetLastError();
+}
+
+// glm_topk_slots (source/glm_glue.cu:429-444): k -> cache slot block_table[row_seq[r]][k / 64] * 64 + k % 64.
+__global__ __launch_bounds__(256) void kg_topk_slots_kernel(int* __restrict__ ind, const int* __restrict__ block_table,
+                                                            int max_pages, const int* __restrict__ row_seq,
+                                                            const int* __restrict__ klen, int* __restrict__ tlen,
+                                                            int T) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= T) return;
+  const int* bt = block_table + (size_t)row_seq[r] * max_pages;
+  int4* row = reinterpret_cast<int4*>(ind + (size_t)r * KG_TOPK);
+  auto map = [&](int k) { return k < 0 ? -1 : bt[k / KG_PAGE] * KG_PAGE + k % KG_PAGE; };
+#pragma unroll
+  for (int i = 0; i < KG_TOPK / 4 / 64; ++i) {
+    int4 v = row[i * 64 + lane];
+    v.x = map(v.x), v.y = map(v.y), v.z = map(v.z), v.w = map(v.w);
+    row[i * 64 + lane] = v;
+  }
+  if (lane == 0) tlen[r] = min(klen[r], KG_TOPK);
+}
+
+extern "C" int kg_topk_slots(int* ind, const int* block_table, int max_pages, const int* row_seq, const int* klen,
+                             int* tlen, int T, void* stream) {
+  KG_CHECK(ind && block_table && row_seq && klen && tlen && T >= 0 && max_pages > 0 && kg_aligned(ind, 16));
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(kg_topk_slots_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, ind, block_table,
+                     max_pages, row_seq, klen, tlen, T);
+  return (int)hipGetLastError();
+}
+
+// ============================================================================ cache gathers
+
+// Block b of a launch -> (sequence s, its page j, the stream row of the page's first row), as the reference
+// walks the sequences (source/glm_glue.cu:360-367); false past the last page.
+KG_DEV bool kg_page_of(int b, const int* seq_lens, int nseq, int& s, int& j, unsigned& row0, int& n) {
+  unsigned goff = 0;
+  for (s = 0; s < nseq; ++s) {
+    const int len = seq_lens[s], pages = (len + KG_PAGE - 1) / KG_PAGE;
+    if (b < pages) {
+      j = b;
+      row0 = goff + (unsigned)(b * KG_PAGE);
+      n = min(KG_PAGE, len - b * KG_PAGE);
+      return true;
+    }
+    b -= pages;
+    goff += (unsigned)len;
+  }
+  return false;
+}
+
+// glm_idx_gather (source/glm_glue.cu:353-376): a workgroup per page, 16 bytes per thread, the scales by
+// the first n threads.
+__global__ __launch_bounds__(256) void kg_idx_gather_kernel(const u8* __restrict__ idx, const int* __restrict__ block_table,
+                                                            int max_pages, const int* __restrict__ seq_lens, int nseq,
+                                                            u8* __restrict__ kg, float* __restrict__ ksf) {
+  int s, j, n;
+  unsigned row0;
+  if (!kg_page_of((int)blockIdx.x, seq_lens, nseq, s, j, row0, n)) return;
+  const u8* src = idx + (size_t)block_table[(size_t)s * max_pages + j] * KG_IDX_PAGE;
+  const uint4* sv = reinterpret_cast<const uint4*>(src);
+  uint4* dv = reinterpret_cast<uint4*>(kg + (size_t)row0 * KG_ID);
+  for (int i = threadIdx.x; i < n * (KG_ID / 16); i += 256) dv[i] = sv[i];
+  if ((int)threadIdx.x < n) ksf[row0 + threadIdx.x] = reinterpret_cast<const float*>(src + KG_PAGE * KG_ID)[threadIdx.x];
+}
+
+extern "C" int kg_idx_gather(const void* idx, const int* block_table, int max_pages, const int* seq_lens, int nseq,
+                             void* kg, float* ksf, int blocks, void* stream) {
+  KG_CHECK(idx && block_table && seq_lens && kg && ksf && max_pages > 0 && nseq >= 0 && blocks >= 0);
+  KG_CHECK(kg_aligned(idx, 16) && kg_aligned(kg, 16));
+  if (blocks == 0) return 0;
+  hipLaunchKernelGGL(kg_idx_gather_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const u8*)idx,
+                     block_table, max_pages, seq_lens, nseq, (u8*)kg, ksf);
+  return (int)hipGetLastError();
+}
+
+// glm_kv_dequant (source/glm_glue.cu:378-414): fp8 latent rows -> bf16 [576] rows of the stream, value =
+// bf16(f32(e4m3) * tile scale), k_pe copied.  A workgroup per page, a 32-lane half wave per row: lane l
+// converts 16 codes (tile l >> 3) into 32 bytes, lanes 0-7 copy the 128 bytes of k_pe.
+__global__ __launch_bounds__(256) void kg_kv_dequant_kernel(const u8* __restrict__ kv, const int* __restrict__ block_table,
+                                                            int max_pages, const int* __restrict__ seq_lens, int nseq,
+                                                            u16* __restrict__ kvd) {
+  int s, j, n;
+  unsigned row0;
+  if (!kg_page_of((int)blockIdx.x, seq_lens, nseq, s, j, row0, n)) return;
+  const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const u8* page = kv + (size_t)block_table[(size_t)s * max_pages + j] * KG_PAGE * KG_KV8;
+  for (int i = hw; i < n; i += 8) {
+    const u8* src = page + (size_t)i * KG_KV8;
+    u8* dst = reinterpret_cast<u8*>(kvd + ((size_t)row0 + i) * KG_MLA);
+    const uint4 q = *reinterpret_cast<const uint4*>(src + l * 16);
+    const float sc = reinterpret_cast<const float*>(src + KG_KVL)[l >> 3];
+    const u32 qw[4] = {q.x, q.y, q.z, q.w};
+    u32 o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const u32 b0 = (qw[k >> 1] >> (16 * (k & 1))) & 0xffu, b1 = (qw[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;
+      o[k] = kg_pack_bf16x2(kg_e4m3_to_f32(b0) * sc, kg_e4m3_to_f32(b1) * sc);
+    }
+    reinterpret_cast<uint4*>(dst + l * 32)[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    reinterpret_cast<uint4*>(dst + l * 32)[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    if (l < 8) reinterpret_cast<uint4*>(dst + KG_KVL * 2)[l] = reinterpret_cast<const uint4*>(src + KG_KVL + 16)[l];
+  }
+}
+
+extern "C" int kg_kv_dequant(const void* kv, const int* block_table, int max_pages, const int* seq_lens, int nseq,
+                             void* kvd, int blocks, void* stream) {
+  KG_CHECK(kv && block_table && seq_lens && kvd && max_pages > 0 && nseq >= 0 && blocks >= 0);
+  KG_CHECK(kg_aligned(kv, 16) && kg_aligned(kvd, 16));
+  if (blocks == 0) return 0;
+  hipLaunchKernelGGL(kg_kv_dequant_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const u8*)kv,
+                     block_table, max_pages, seq_lens, nseq, (u16*)kvd);
+  return (int)hipGetLastError();
+}

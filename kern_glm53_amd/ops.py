@@ -16,7 +16,7 @@ from ._lib import call
 __all__ = [
     "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "bf16_batched", "mqa_logits", "quant",
     "silu_mul_quant", "routing", "moe_psum", "moe_gather", "moe_combine", "router_topk", "requant", "kvb",
-    "add_rms_quant", "mla_prep", "q_post",
+    "add_rms_quant", "mla_prep", "q_post", "topk_prefill", "topk_stream", "topk_slots", "idx_gather", "kv_dequant",
     "sf_words", "counts_len", "EXPERTS", "TOPK", "TILE",
 ]
 
@@ -113,6 +113,36 @@ def q_post(qb, ldb: int, rope, pos, qmla, iq, iw, wout, full: int, T: int, *, ro
     """glm_q_post (source/glm_glue.cu:301-351); full = 0 with iq / iw / wout None is `q_post_shared`."""
     call("kg_q_post", _ptr(qb), ldb, _ptr(rope), _ptr(pos), _ptr(qmla), _ptr(iq), _ptr(iw), _ptr(wout), full, T,
          rope_rows, _stream())
+
+
+def topk_prefill(logits, starts, ends, out, num_rows: int, stride0: int, *, stride1: int = 1, topk: int = 2048,
+                 offset: int = 0):
+    """The `glm_topk_prefill` launch of the `indexer` op (scripts/glm_ops.py:123-127): the top-k indices of each
+    compressed logits row, ascending (ties toward the smallest index)."""
+    call("kg_topk_prefill", _ptr(logits), _ptr(starts), _ptr(ends), _ptr(out), num_rows, stride0, stride1, topk,
+         offset, _stream())
+
+
+def topk_stream(ind, ks, klen, tlen, T: int):
+    """glm_topk_stream (source/glm_glue.cu:416-427)."""
+    call("kg_topk_stream", _ptr(ind), _ptr(ks), _ptr(klen), _ptr(tlen), T, _stream())
+
+
+def topk_slots(ind, block_table, max_pages: int, row_seq, klen, tlen, T: int):
+    """glm_topk_slots (source/glm_glue.cu:429-444)."""
+    call("kg_topk_slots", _ptr(ind), _ptr(block_table), max_pages, _ptr(row_seq), _ptr(klen), _ptr(tlen), T,
+         _stream())
+
+
+def idx_gather(idx, block_table, max_pages: int, seq_lens, nseq: int, kg, ksf, *, blocks: int):
+    """glm_idx_gather (source/glm_glue.cu:353-376); blocks = ceil(ctx / 64) + nseq as the op's grid."""
+    call("kg_idx_gather", _ptr(idx), _ptr(block_table), max_pages, _ptr(seq_lens), nseq, _ptr(kg), _ptr(ksf), blocks,
+         _stream())
+
+
+def kv_dequant(kv, block_table, max_pages: int, seq_lens, nseq: int, kvd, *, blocks: int):
+    """glm_kv_dequant (source/glm_glue.cu:378-414)."""
+    call("kg_kv_dequant", _ptr(kv), _ptr(block_table), max_pages, _ptr(seq_lens), nseq, _ptr(kvd), blocks, _stream())
 
 
 def routing(ids, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, *, T: int,

@@ -9,6 +9,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 typedef uint8_t u8;
@@ -566,6 +567,121 @@ void kgo_q_post(const u16* qb, int ldb, const u16* rope, const int* pos, u16* qm
       w *= 0.17677669529663687f;
       wout[(size_t)r * KGO_IH + ih] = w;
     }
+  }
+}
+
+/* ---------------------------------------------------------------- indexer consumers (f2) */
+
+#define KGO_TOPK 2048     /* the attention's key budget: source/glm_glue.cu:36 */
+
+/* The reference's total order on logits (sampler_topk.cuh:19-31): its transform of the f32 bits ranks
+ * a larger float first and -0 after +0; as an unsigned key (larger = earlier) that is the bits with the
+ * sign bit flipped for non-negative values and all bits flipped for negative ones. */
+static inline u32 topk_key(float x) {
+  const u32 b = f2u(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+static int cmp_u64_desc(const void* a, const void* b) {
+  const unsigned long long x = *(const unsigned long long*)a, y = *(const unsigned long long*)b;
+  return x < y ? 1 : (x > y ? -1 : 0);
+}
+static int cmp_int_asc(const void* a, const void* b) {
+  const int x = *(const int*)a, y = *(const int*)b;
+  return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* vLLM's prefill top-k as glm_topk_prefill launches it (source/vllm-topk/topk.cu:18-35 over
+ * sampler_topk.cuh:297-547, stride1 = 1): for rows r = offset + i, i < num_rows, of logits (stride0 apart),
+ * elements [starts[r], ends[r]).  A row of len <= topk gives 0 .. len-1 then -1 (sampler_topk.cuh:355-374);
+ * otherwise the topk indices (relative to the start) of its largest values in the order above.  The
+ * reference's choice among values tied at the threshold, and the order it lists them in, follow its
+ * atomics; this restatement (and the kernel) take ties toward the smallest index and list the indices
+ * ascending. */
+void kgo_topk_prefill(const float* logits, const int* starts, const int* ends, int* out, int num_rows, int stride0,
+                      int topk, int offset) {
+  for (int i = 0; i < num_rows; ++i) {
+    const int r = offset + i, start = starts[r];
+    const int len = ends[r] - start > 0 ? ends[r] - start : 0;
+    int* o = out + (size_t)r * topk;
+    if (len <= topk) {
+      for (int k = 0; k < topk; ++k) o[k] = k < len ? k : -1;
+      continue;
+    }
+    unsigned long long* c = (unsigned long long*)malloc(sizeof(unsigned long long) * (size_t)len);
+    const float* row = logits + (size_t)r * stride0 + start;
+    /* key descending, then index ascending: (key << 32) | (2^32 - 1 - index), sorted descending */
+    for (int e = 0; e < len; ++e) c[e] = ((unsigned long long)topk_key(row[e]) << 32) | (0xffffffffu - (u32)e);
+    qsort(c, (size_t)len, sizeof *c, cmp_u64_desc);
+    for (int k = 0; k < topk; ++k) o[k] = (int)(0xffffffffu - (u32)(c[k] & 0xffffffffu));
+    qsort(o, (size_t)topk, sizeof *o, cmp_int_asc);
+    free(c);
+  }
+}
+
+/* glm_topk_stream, source/glm_glue.cu:416-427. */
+void kgo_topk_stream(int* ind, const u32* ks, const int* klen, int* tlen, int T) {
+  for (int r = 0; r < T; ++r) {
+    for (int i = 0; i < KGO_TOPK; ++i) {
+      const int k = ind[(size_t)r * KGO_TOPK + i];
+      ind[(size_t)r * KGO_TOPK + i] = k < 0 ? -1 : (int)ks[r] + k;
+    }
+    tlen[r] = klen[r] < KGO_TOPK ? klen[r] : KGO_TOPK;
+  }
+}
+
+/* glm_topk_slots, source/glm_glue.cu:429-444. */
+void kgo_topk_slots(int* ind, const int* block_table, int max_pages, const int* row_seq, const int* klen, int* tlen,
+                    int T) {
+  for (int r = 0; r < T; ++r) {
+    const int* bt = block_table + (size_t)row_seq[r] * max_pages;
+    for (int i = 0; i < KGO_TOPK; ++i) {
+      const int k = ind[(size_t)r * KGO_TOPK + i];
+      ind[(size_t)r * KGO_TOPK + i] = k < 0 ? -1 : bt[k / KGO_PAGE] * KGO_PAGE + k % KGO_PAGE;
+    }
+    tlen[r] = klen[r] < KGO_TOPK ? klen[r] : KGO_TOPK;
+  }
+}
+
+/* glm_idx_gather, source/glm_glue.cu:353-376: page j of sequence s (rows [64 j, min(64 j + 64, len)))
+ * to stream rows goff(s) + 64 j of kg [.][128] and ksf. */
+void kgo_idx_gather(const u8* idx, const int* block_table, int max_pages, const int* seq_lens, int nseq, u8* kg,
+                    float* ksf) {
+  unsigned goff = 0;
+  for (int s = 0; s < nseq; ++s) {
+    const int len = seq_lens[s], pages = (len + KGO_PAGE - 1) / KGO_PAGE;
+    for (int j = 0; j < pages; ++j) {
+      const u8* src = idx + (size_t)block_table[(size_t)s * max_pages + j] * KGO_IDX_PAGE;
+      const int n = len - j * KGO_PAGE < KGO_PAGE ? len - j * KGO_PAGE : KGO_PAGE;
+      const size_t d = goff + (size_t)j * KGO_PAGE;
+      memcpy(kg + d * KGO_ID, src, (size_t)n * KGO_ID);
+      memcpy(ksf + d, src + KGO_PAGE * KGO_ID, (size_t)n * 4);
+    }
+    goff += (unsigned)len;
+  }
+}
+
+/* glm_kv_dequant, source/glm_glue.cu:378-414: fp8 latent rows to bf16 [576] stream rows, each value
+ * bf16(f32(e4m3) * its 128-column tile's scale), k_pe's 64 bf16 copied. */
+void kgo_kv_dequant(const u8* kv, const int* block_table, int max_pages, const int* seq_lens, int nseq, u16* kvd) {
+  unsigned goff = 0;
+  for (int s = 0; s < nseq; ++s) {
+    const int len = seq_lens[s], pages = (len + KGO_PAGE - 1) / KGO_PAGE;
+    for (int j = 0; j < pages; ++j) {
+      const u8* page = kv + (size_t)block_table[(size_t)s * max_pages + j] * KGO_PAGE * KGO_KV8;
+      const int n = len - j * KGO_PAGE < KGO_PAGE ? len - j * KGO_PAGE : KGO_PAGE;
+      for (int i = 0; i < n; ++i) {
+        const u8* src = page + (size_t)i * KGO_KV8;
+        u16* dst = kvd + (goff + (size_t)j * KGO_PAGE + i) * KGO_MLA;
+        for (int c = 0; c < KGO_KVL; ++c) {
+          float sc;
+          memcpy(&sc, src + KGO_KVL + 4 * (c >> 7), 4);
+          dst[c] = kgo_f32_to_bf16(kgo_e4m3_to_f32(src[c]) * sc);
+        }
+        memcpy(dst + KGO_KVL, src + KGO_KVL + 16, 128);
+      }
+    }
+    goff += (unsigned)len;
   }
 }
 

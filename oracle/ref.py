@@ -271,6 +271,57 @@ def q_post(qb, rope, pos, qmla, iq, iw, wout, full: bool, T: int):
                      ctypes.c_int(T), ctypes.c_int(rope.shape[0]))
 
 
+# ------------------------------------------------------------------ indexer consumers (f2)
+
+def topk_prefill(logits, starts, ends, topk: int = 2048, num_rows=None, offset: int = 0, out=None):
+    """glm_topk_prefill (source/vllm-topk/topk.cu:18-35): logits f32 [rows][stride0]; out int32 [rows][topk]
+    (rows offset .. offset + num_rows written)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    st = np.ascontiguousarray(starts, dtype=np.int32)
+    en = np.ascontiguousarray(ends, dtype=np.int32)
+    rows = lg.shape[0]
+    num_rows = rows - offset if num_rows is None else num_rows
+    out = np.full((rows, topk), -7, dtype=np.int32) if out is None else out
+    lib().kgo_topk_prefill(_p(lg), _p(st), _p(en), _p(out), ctypes.c_int(num_rows), ctypes.c_int(lg.shape[1]),
+                           ctypes.c_int(topk), ctypes.c_int(offset))
+    return out
+
+
+def topk_stream(ind, ks, klen):
+    """glm_topk_stream (source/glm_glue.cu:416-427), in place on ind [T][2048]; returns tlen."""
+    T = ind.shape[0]
+    tlen = np.empty(T, dtype=np.int32)
+    lib().kgo_topk_stream(_p(ind), _p(np.ascontiguousarray(ks, dtype=np.uint32)),
+                          _p(np.ascontiguousarray(klen, dtype=np.int32)), _p(tlen), ctypes.c_int(T))
+    return tlen
+
+
+def topk_slots(ind, block_table, row_seq, klen):
+    """glm_topk_slots (source/glm_glue.cu:429-444), in place on ind [T][2048]; returns tlen."""
+    T = ind.shape[0]
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    tlen = np.empty(T, dtype=np.int32)
+    lib().kgo_topk_slots(_p(ind), _p(bt), ctypes.c_int(bt.shape[1]), _p(np.ascontiguousarray(row_seq, dtype=np.int32)),
+                         _p(np.ascontiguousarray(klen, dtype=np.int32)), _p(tlen), ctypes.c_int(T))
+    return tlen
+
+
+def idx_gather(idx_pages, block_table, seq_lens, kg, ksf):
+    """glm_idx_gather (source/glm_glue.cu:353-376) into kg uint8 [rows][128] / ksf f32 [rows], in place."""
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    lib().kgo_idx_gather(_p(np.ascontiguousarray(idx_pages, dtype=np.uint8)), _p(bt), ctypes.c_int(bt.shape[1]), _p(sl),
+                         ctypes.c_int(len(sl)), _p(kg), _p(ksf))
+
+
+def kv_dequant(kv_pages, block_table, seq_lens, kvd):
+    """glm_kv_dequant (source/glm_glue.cu:378-414) into kvd bf16 bits [rows][576], in place."""
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    lib().kgo_kv_dequant(_p(np.ascontiguousarray(kv_pages, dtype=np.uint8)), _p(bt), ctypes.c_int(bt.shape[1]), _p(sl),
+                         ctypes.c_int(len(sl)), _p(kvd))
+
+
 # ------------------------------------------------------------------ weight layout (a12, a13)
 
 def requant(w8, s, wq, sf, rows, K, group_rows, dst_group_rows=0, dst_row0=0, sf_ld=None, sf_group=0):

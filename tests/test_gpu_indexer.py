@@ -1,0 +1,155 @@
+"""GPU parity of the indexer consumers against the oracle, bit for bit: the prefill top-k (short rows, rows
+of exactly K and K + 1, full 65536-element rows, unaligned starts, rows longer than 65536 through the
+streaming variant, heavy ties, signed zeros, the offset / num_rows window), the index maps and the paged
+cache gathers; plus the top-k of the indexer's own MQA logits at the 16384-row chunk, sampled."""
+import numpy as np
+import pytest
+import torch
+
+from kern_glm53_amd import ops
+from oracle import ref
+from tests._gpu import DEV, d, h
+
+pytestmark = pytest.mark.gpu
+
+
+def run_topk(logits, starts, ends, k, num_rows=None, offset=0):
+    R, stride0 = logits.shape
+    num_rows = R - offset if num_rows is None else num_rows
+    out_ref = ref.topk_prefill(logits, starts, ends, k, num_rows=num_rows, offset=offset)
+    out = torch.full((R, k), -7, dtype=torch.int32, device=DEV)
+    ops.topk_prefill(d(logits), d(starts), d(ends), out, num_rows, stride0, topk=k, offset=offset)
+    got = h(out, np.int32)
+    return got, out_ref
+
+
+@pytest.mark.parametrize("case", ["mixed", "full", "ties", "unaligned", "long", "window", "k256"])
+def test_topk_prefill_bit_exact(case):
+    print(f"topk_prefill case={case}", flush=True)
+    rng = np.random.default_rng(sum(map(ord, case)))
+    k = 2048
+    if case == "mixed":
+        lens = [0, 1, 2047, 2048, 2049, 4096, 30000, 57344, 49153, 65533]
+        stride0 = 65536
+    elif case == "full":
+        lens, stride0 = [65536] * 6, 65536
+    elif case == "ties":
+        lens, stride0 = [60000, 20000, 3000, 65536], 65536
+    elif case == "unaligned":
+        lens, stride0 = [40000, 40001, 40002, 5000], 40008
+    elif case == "long":
+        lens, stride0 = [70000, 131072, 66000, 100], 131072
+    elif case == "window":
+        lens, stride0 = [5000] * 8, 5120
+    else:
+        lens, stride0, k = [300, 256, 257, 9000], 9000, 256
+    R = len(lens)
+    logits = (rng.standard_normal((R, stride0)) * rng.uniform(0.01, 100, (R, 1))).astype(np.float32)
+    starts = np.zeros(R, np.int32)
+    if case == "ties":
+        logits = np.round(logits * 3).astype(np.float32)
+        logits[1] = 1.0
+        logits[1, ::7] = 2.0
+        logits[2, :] = 0.0
+        logits[2, ::3] = -0.0
+    if case == "unaligned":
+        starts = np.array([1, 2, 3, 5], np.int32)
+    ends = (starts + np.array(lens)).astype(np.int32)
+    if case == "window":
+        got, exp = run_topk(logits, starts, ends, k, num_rows=3, offset=4)
+    else:
+        got, exp = run_topk(logits, starts, ends, k)
+    for r in range(R):
+        assert np.array_equal(got[r], exp[r]), (case, r, lens[r] if r < len(lens) else None)
+
+
+def test_topk_prefill_mqa_chunk_sampled():
+    """The top-k of the indexer's compressed logits at the chunk the bench runs: 16384 rows of one
+    65536-token sequence (row r scores keys [0, 49153 + r)), logits from kg_mqa_logits; 24 rows against the
+    oracle, every row's count of taken indices checked."""
+    from kern_glm53_amd import synth
+
+    M, ctx = 16384, 65536
+    print("topk over mqa logits 16384 x 65536", flush=True)
+    g = synth.generator(900, "cuda")
+    codes = lambda *s: (torch.randint(0, 0x78, s, generator=g, device=DEV, dtype=torch.int32)
+                        | (torch.randint(0, 2, s, generator=g, device=DEV, dtype=torch.int32) << 7)).to(torch.uint8)
+    iq, kg = codes(M, 32, 128), codes(ctx, 128)
+    ksf = torch.exp2(torch.randint(-8, 0, (ctx,), generator=g, device=DEV).float())
+    w = torch.randn(M, 32, generator=g, device=DEV) * (128 ** -0.5) * (32 ** -0.5)
+    ks = torch.zeros(M, dtype=torch.int32, device=DEV)
+    ke = torch.arange(M, dtype=torch.int32, device=DEV) + (ctx - M) + 1
+    logits = torch.empty(M, ctx, dtype=torch.float32, device=DEV)
+    ops.mqa_logits(iq, kg, ksf, w, ks, ke, logits, M, ctx, ctx)
+    out = torch.empty(M, 2048, dtype=torch.int32, device=DEV)
+    zero = torch.zeros(M, dtype=torch.int32, device=DEV)
+    klen = ke - ks
+    ops.topk_prefill(logits, zero, klen, out, M, ctx)
+    rows = sorted(np.random.default_rng(3).choice(M, 24, replace=False).tolist())
+    lg = h(logits[rows], np.float32)
+    exp = ref.topk_prefill(lg, np.zeros(len(rows), np.int32), h(klen[rows], np.int32))
+    assert np.array_equal(h(out[rows], np.int32), exp)
+    o = out.cpu()
+    assert bool(((o >= 0) & (o < klen.cpu()[:, None])).all())                 # every index taken, in range
+    assert bool((o[:, 1:] > o[:, :-1]).all())                                  # ascending, distinct
+
+
+def test_topk_stream_and_slots_bit_exact():
+    print("topk_stream / topk_slots", flush=True)
+    rng = np.random.default_rng(11)
+    T = 37
+    ind = rng.integers(-1, 70000, (T, 2048)).astype(np.int32)
+    ks = rng.integers(0, 1 << 20, T).astype(np.uint32)
+    klen = rng.integers(0, 5000, T).astype(np.int32)
+    a = ind.copy()
+    tl = ref.topk_stream(a, ks, klen)
+    ind_d, tl_d = d(ind), torch.zeros(T, dtype=torch.int32, device=DEV)
+    ops.topk_stream(ind_d, d(ks), d(klen), tl_d, T)
+    assert np.array_equal(h(ind_d, np.int32), a) and np.array_equal(h(tl_d, np.int32), tl)
+    bt = rng.integers(0, 5000, (4, 1100)).astype(np.int32)
+    row_seq = rng.integers(0, 4, T).astype(np.int32)
+    b = ind.copy()
+    tl = ref.topk_slots(b, bt, row_seq, klen)
+    ind_d, tl_d = d(ind), torch.zeros(T, dtype=torch.int32, device=DEV)
+    ops.topk_slots(ind_d, d(bt), bt.shape[1], d(row_seq), d(klen), tl_d, T)
+    assert np.array_equal(h(ind_d, np.int32), b) and np.array_equal(h(tl_d, np.int32), tl)
+
+
+def paged(rng, seq_lens, n_pages):
+    pages_per = [(l + 63) // 64 for l in seq_lens]
+    bt = np.full((len(seq_lens), max(pages_per) + 2), -1, np.int32)
+    perm = rng.permutation(n_pages)
+    c = 0
+    for s, p in enumerate(pages_per):
+        bt[s, :p] = perm[c:c + p]
+        c += p
+    return bt
+
+
+@pytest.mark.parametrize("seq_lens", [[130, 64, 1, 200], [65536], [1000, 1, 63, 65, 4097]])
+def test_idx_gather_and_kv_dequant_bit_exact(seq_lens):
+    print(f"idx_gather / kv_dequant seq_lens={seq_lens}", flush=True)
+    rng = np.random.default_rng(sum(seq_lens))
+    n_pages = sum((l + 63) // 64 for l in seq_lens) + 3
+    bt = paged(rng, seq_lens, n_pages)
+    rows = sum(seq_lens)
+    blocks = (rows + 63) // 64 + len(seq_lens) + 2          # the reference's grid, and a little more
+    idx = rng.integers(0, 256, n_pages * ref.IDX_PAGE).astype(np.uint8)
+    kg_ref = np.full((rows, 128), 0xcd, np.uint8)
+    ksf_ref = np.full(rows, -1.0, np.float32)
+    ref.idx_gather(idx, bt, seq_lens, kg_ref, ksf_ref)
+    kg_d = torch.full((rows, 128), 0xcd, dtype=torch.uint8, device=DEV)
+    ksf_d = torch.full((rows,), -1.0, dtype=torch.float32, device=DEV)
+    sl = np.array(seq_lens, np.int32)
+    ops.idx_gather(d(idx), d(bt), bt.shape[1], d(sl), len(seq_lens), kg_d, ksf_d, blocks=blocks)
+    assert np.array_equal(h(kg_d, np.uint8), kg_ref)
+    assert np.array_equal(h(ksf_d, np.uint32), ksf_ref.view(np.uint32))
+    kv = rng.integers(0, 256, (n_pages * 64, 656)).astype(np.uint8)
+    c = kv[:, :512]
+    c[(c & 0x7f) == 0x7f] = 0x33
+    kv[:, 512:528] = (rng.uniform(0.01, 3, (n_pages * 64, 4)).astype(np.float32)).view(np.uint8)
+    kvd_ref = np.zeros((rows, 576), np.uint16)
+    ref.kv_dequant(kv, bt, seq_lens, kvd_ref)
+    kvd_d = torch.zeros(rows, 576, dtype=torch.int16, device=DEV)
+    ops.kv_dequant(d(kv), d(bt), bt.shape[1], d(sl), len(seq_lens), kvd_d, blocks=blocks)
+    assert np.array_equal(h(kvd_d, np.uint16), kvd_ref)
