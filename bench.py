@@ -257,6 +257,8 @@ def aux_prepare(data, dev):
     aux["logits"] = torch.empty(M, ctx, dtype=torch.float32, device=dev)
     aux["ctx"] = ctx
     aux["klen"] = sum(range(ctx - M + 1, ctx + 1))
+    aux["klen_t"] = aux["ke"] - aux["ks"]
+    aux["ind"] = torch.empty(M, 2048, dtype=torch.int32, device=dev)
     return aux
 
 
@@ -277,6 +279,9 @@ def aux_launches(aux):
         ("mqa_logits", lambda: ops.mqa_logits(aux["iq"], aux["kg"], aux["ksf"], aux["w"], aux["ks"], aux["ke"],
                                               aux["logits"], M, ctx, ctx),
          2.0 * 128 * 32 * klen, 4 * klen + M * 32 * 128 + ctx * 132 + M * 136, "mfma"),
+        # the indexer's consumer of those logits: read every compressed row once, write 2048 indices a row
+        ("topk_prefill", lambda: ops.topk_prefill(aux["logits"], aux["ks"], aux["klen_t"], aux["ind"], M, ctx),
+         0.0, 4 * klen + M * 2048 * 4 + M * 8, "hbm"),
     ]
 
 

@@ -132,8 +132,8 @@ int kg_q_post(const void* qb, int ldb, const void* rope, const int* pos, void* q
  * (stride0 floats apart), elements [starts[r], ends[r]): out[r][0:topk] = the topk indices (relative to
  * starts[r]) of the largest values, ascending, ties at the threshold toward the smallest index (the
  * reference lists the same set, up to its ties, in its atomics' order); a row of at most topk elements
- * gives 0 .. len-1 then -1.  Requires stride1 == 1 (the op's), stride0 % 4 == 0, logits 16-byte aligned,
- * topk <= 8192, and every row inside its stride0 floats. */
+ * gives 0 .. len-1 then -1.  Requires stride1 == 1 (the op's), stride0 % 4 == 0, logits 16-byte aligned
+ * and every row inside its stride0 floats. */
 int kg_topk_prefill(const float* logits, const int* starts, const int* ends, int* out, int num_rows, int stride0,
                     int stride1, int topk, int offset, void* stream);
 

@@ -16,9 +16,10 @@
 
 // ============================================================================ top-k
 
-// One 1024-thread workgroup per row.  A row of up to 65536 logits is read once into registers: thread t
-// holds elements [64 t, 64 t + 64) of a segment, so thread order is index order.  Longer rows are
-// processed in segments of 65536, re-read from memory on each pass.
+// One 1024-thread workgroup per row.  A row of up to 65536 logits is read once, coalesced, into registers:
+// element e = 4 (1024 i + t) + c of a segment (in coordinates from the 16-byte aligned origin at or below
+// the row start) is key[4 i + c] of thread t.  Longer rows are processed in segments of 65536 elements,
+// re-read on each pass.
 //
 // Selection is a radix select over the order-preserving key of the f32 bits (larger float, larger key;
 // -0 below +0, as the reference's bit transform orders them).  Valid keys are clamped to at least 1 (only a
@@ -27,15 +28,22 @@
 // of the row's smallest and largest valid keys are resolved at most 11 at a time: each pass histograms the
 // candidates' next bits (four interleaved copies, lane & 3, spreading a hot bin's atomics over four banks;
 // non-candidates add to a per-lane dummy slot, so the loop has no branches), then a block-wide suffix scan
-// finds the bin holding the K-th largest.  A pass ends the search early when that bin's elements are exactly
-// the ones still needed.  Output: the K selected indices (relative to the row start) in ascending order,
-// ties at the threshold broken toward the smallest index, staged in LDS and stored coalesced; rows of at
-// most K elements give 0 .. len-1 then -1 (the reference's shortcut).  The reference emits the same set up
-// to its ties, in the order its atomics happen to produce.
+// finds the bin holding the K-th largest.  After the first pass the bin's elements (when at most 8192) are
+// compacted into an LDS list, over which the later passes run.  A pass ends the search early when its bin
+// holds exactly the elements still needed.
+//
+// Output: the K selected indices (relative to the row start) in ascending order, ties at the threshold
+// broken toward the smallest index.  Taken elements set their bit in a 65536-bit LDS bitmap (8 lanes hold
+// one 32-bit word's 32 elements and assemble it by DPP, so there are no atomics); a popcount scan of the
+// words gives every index its position.  Ties use a second bitmap of the threshold's equal elements, of
+// which the first `need` in index order are added.  Rows of at most K elements give 0 .. len-1 then -1
+// (the reference's shortcut).  The reference emits the same set up to its ties, in the order its atomics
+// happen to produce.
 #define KG_TK_T 1024
 #define KG_TK_V 64
 #define KG_TK_SEG (KG_TK_T * KG_TK_V)
-#define KG_TK_LDS 8192                 // histogram copies (4 x 2048), reused as the output staging area
+#define KG_TK_HIST 8192                // histogram copies (4 x 2048); then the two bitmaps (2 x 2048 words)
+#define KG_TK_CAND 8192                // candidate list after the first pass
 
 KG_DEV u32 kg_okey(float f) {
   const u32 b = kg_f2u(f);
@@ -65,14 +73,127 @@ KG_DEV int kg_tk_scan(int v, int* wsum, int& tot) {
   return base + inc - v;
 }
 
-// MULTI = false: the row (end - start <= stride0 <= 65536) is held in registers; true: segments of 65536 are
-// re-read on every pass (stride0 > 65536).
+// OR over each group of 8 lanes (DPP: quad xor 1, quad xor 2, then the half-row mirror).
+KG_DEV u32 kg_or8(u32 v) {
+  v |= (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false);
+  v |= (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false);
+  v |= (u32)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false);
+  return v;
+}
+
+// One radix pass: histogram of the candidates' next wd bits (candidates: (key & m) == pm) fed by `feed`,
+// which calls its argument on every key; then the bin holding the need-th largest.  Updates pm, m, s, need
+// and sets cnt to that bin's count.
+template <class Feed>
+KG_DEV void kg_tk_pass(Feed feed, u32* lds, int* wsum, int* found, u32& pm, u32& m, int& s, int& need, int& cnt) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
+  for (int i = t; i < 4 * NB; i += KG_TK_T) lds[i] = 0;
+  __syncthreads();
+  const u32 m0 = m, pm0 = pm;
+  feed([&](u32 k) {
+    const int slot = (k & m0) == pm0 ? (int)((((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
+                                     : KG_TK_HIST + lane;
+    __hip_atomic_fetch_add(&lds[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  });
+  __syncthreads();
+  // descending bins: thread t sums bins NB-1-2t and NB-2-2t (NB is even)
+  int hh = 0, hl = 0;
+  if (2 * t < NB) {
+    const uint4 a = *reinterpret_cast<const uint4*>(&lds[(NB - 1 - 2 * t) << 2]);
+    const uint4 b = *reinterpret_cast<const uint4*>(&lds[(NB - 2 - 2 * t) << 2]);
+    hh = (int)((a.x + a.y) + (a.z + a.w));
+    hl = (int)((b.x + b.y) + (b.z + b.w));
+  }
+  int tot;
+  const int above = kg_tk_scan(hh + hl, wsum, tot);
+  if (2 * t < NB) {
+    if (above < need && need <= above + hh) found[0] = NB - 1 - 2 * t, found[1] = above, found[2] = hh;
+    else if (above + hh < need && need <= above + hh + hl) found[0] = NB - 2 - 2 * t, found[1] = above + hh, found[2] = hl;
+  }
+  __syncthreads();
+  const int b = found[0], ab = found[1];
+  cnt = found[2];
+  __syncthreads();
+  need -= ab;
+  pm |= (u32)b << s2;
+  m = 0xffffffffu << s2;
+  s = s2;
+}
+
+// Writes the row's indices from the taken bitmap (2048 words: bit e of the 65536 elements of segment `seg`,
+// in aligned coordinates), after choosing the first `need - eq_base` set bits of the equal-element bitmap
+// when `ties`.  Returns the number of indices written (out_base advances by it).
+KG_DEV void kg_tk_emit(u32* taken, u32* eqbm, bool ties, int need, int& eq_base, int& out_base, int* wsum, int* orow,
+                       int seg, int lo) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  u32 w0 = taken[2 * t], w1 = taken[2 * t + 1];   // thread t: elements 64 t .. 64 t + 63
+  if (ties) {                                      // the first `need` equal elements in index order
+    u32 e0 = eqbm[2 * t], e1 = eqbm[2 * t + 1];
+    int te;
+    int rank = kg_tk_scan(__builtin_popcount(e0) + __builtin_popcount(e1), wsum, te) + eq_base;
+    while (e0 && rank < need) w0 |= e0 & (0u - e0), e0 &= e0 - 1, ++rank;
+    while (e1 && rank < need) w1 |= e1 & (0u - e1), e1 &= e1 - 1, ++rank;
+    eq_base += te;
+  }
+  int tt;
+  int pos = kg_tk_scan(__builtin_popcount(w0) + __builtin_popcount(w1), wsum, tt) + out_base;
+  const int e0 = seg * KG_TK_SEG + 64 * t - lo;   // index of word 2t's bit 0, relative to the row start
+  while (w0) orow[pos++] = e0 + __builtin_ctz(w0), w0 &= w0 - 1;
+  while (w1) orow[pos++] = e0 + 32 + __builtin_ctz(w1), w1 &= w1 - 1;
+  out_base += tt;
+}
+
+// On one wave: the bin of the need-th largest element among NB bins (bin b's count is the sum of its
+// COPIES words, interleaved).  Lane L takes NB / 64 bins from the top (one bin, or none, when NB < 64), an
+// exclusive scan over lanes finds the lane holding the need-th, which walks its bins.  Wave-uniform results.
+template <int COPIES>
+KG_DEV void kg_tk_wave_find(const u32* hist, int NB, int need, int& bin, int& above, int& cnt) {
+  const int lane = threadIdx.x & 63;
+  const int per = NB >= 64 ? NB / 64 : 1, top = NB - 1 - per * lane;
+  auto count = [&](int b) {
+    u32 c = 0;
+#pragma unroll
+    for (int k = 0; k < COPIES; ++k) c += hist[b * COPIES + k];
+    return (int)c;
+  };
+  int local = 0;
+  if (top >= 0)
+    for (int k = 0; k < per; ++k) local += count(top - k);
+  int inc = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int x = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += x;
+  }
+  int b = -1, ab = 0, c = 0;
+  if (inc - local < need && need <= inc) {
+    int run = inc - local;
+    for (int k = 0; k < per; ++k) {
+      const int h = count(top - k);
+      if (run + h >= need) {
+        b = top - k, ab = run, c = h;
+        break;
+      }
+      run += h;
+    }
+  }
+  const int src = __builtin_ctzll(__ballot(b >= 0));
+  bin = __shfl(b, src, 64), above = __shfl(ab, src, 64), cnt = __shfl(c, src, 64);
+}
+
+// MULTI = false: the row (its end within stride0 <= 65536 floats) is held in registers for the first pass,
+// after which the bin's elements are compacted into LDS (key and index) and the registers die; true:
+// segments of 65536 are re-read on every pass (stride0 > 65536).
 template <bool MULTI>
 __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restrict__ logits,
                                                            const int* __restrict__ starts,
                                                            const int* __restrict__ ends, int* __restrict__ out,
                                                            int stride0, int topk, int offset) {
-  __shared__ __attribute__((aligned(16))) int lds[KG_TK_LDS + 64];   // + a dummy slot per lane
+  __shared__ __attribute__((aligned(16))) u32 lds[KG_TK_HIST + 64];  // + a dummy slot per lane
+  __shared__ u32 ckey[KG_TK_CAND];
+  __shared__ int cidx[KG_TK_CAND];
   __shared__ int wsum[KG_TK_T / 64];
   __shared__ u32 red[2][KG_TK_T / 64];
   __shared__ int found[3];
@@ -84,9 +205,9 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
     for (int i = t; i < topk; i += KG_TK_T) orow[i] = i < len ? i : -1;
     return;
   }
-  // Loads are 16-byte buffer loads from the 16-byte aligned origin a0 <= start (logits is 16-byte aligned
-  // and stride0 % 4 == 0) through a resource covering the valid part of the row, so a vector past it reads
-  // zeros; element i of the aligned row is valid for lo <= i < hi.  (A buffer load is one instruction the
+  // 16-byte buffer loads from the 16-byte aligned origin a0 <= start (logits is 16-byte aligned and
+  // stride0 % 4 == 0) through a resource covering the row up to its end, so a vector past it reads zeros;
+  // element e of the aligned row is valid for lo <= e < hi.  (A buffer load is one instruction the
   // compiler cannot split into conditional scalar loads.)
   const int a0 = start & ~3, lo = start - a0, hi = MULTI ? ends[r] - a0 : min(ends[r] - a0, KG_TK_SEG);
   const __amdgpu_buffer_rsrc_t rrow =
@@ -95,26 +216,54 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
   const int nseg = MULTI ? (hi + KG_TK_SEG - 1) / KG_TK_SEG : 1;
   u32 key[KG_TK_V];
   auto load = [&](int seg) {
-    const int e0 = seg * KG_TK_SEG + t * KG_TK_V;
 #pragma unroll
     for (int i = 0; i < KG_TK_V / 4; ++i) {
-      const auto f = __builtin_amdgcn_raw_buffer_load_b128(rrow, (unsigned)(e0 + 4 * i) * 4u, 0, 0);
+      const int e = seg * KG_TK_SEG + 4 * (KG_TK_T * i + t);
+      const auto f = __builtin_amdgcn_raw_buffer_load_b128(rrow, (unsigned)e * 4u, 0, 0);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const u32 k = kg_okey(kg_u2f(f[c]));
-        key[4 * i + c] = (unsigned)(e0 + 4 * i + c - lo) < (unsigned)(hi - lo) ? k : 0u;   // lo <= e < hi
+        key[4 * i + c] = (unsigned)(e + c - lo) < (unsigned)(hi - lo) ? k : 0u;   // lo <= e + c < hi
       }
     }
   };
-  if (!MULTI) load(0);
+  auto feed_regs = [&](auto f) {
+    for (int seg = 0; seg < nseg; ++seg) {
+      if (MULTI) load(seg);
+#pragma unroll
+      for (int j = 0; j < KG_TK_V; ++j) f(key[j]);
+    }
+  };
+  // taken / equal bits of this thread's elements into the two bitmaps: thread t's nibble of elements
+  // 4 (1024 i + t) .. + 3 is bits 4 (t & 7) .. of word (1024 i + t) / 8, assembled over 8 lanes
+  u32* const taken = lds;
+  u32* const eqbm = lds + 2048;
+  auto mark = [&](u32 m_, u32 pm_, bool eq_taken, bool eq_marked) {
+#pragma unroll
+    for (int i = 0; i < KG_TK_V / 4; ++i) {
+      u32 nt = 0, ne = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32 kk = key[4 * i + c] & m_;
+        nt |= (kk > pm_ || (eq_taken && kk == pm_) ? 1u : 0u) << c;
+        ne |= (kk == pm_ ? 1u : 0u) << c;
+      }
+      nt = kg_or8(nt << (4 * (t & 7)));
+      if ((t & 7) == 0) taken[(KG_TK_T * i + t) >> 3] = nt;
+      if (eq_marked) {
+        ne = kg_or8(ne << (4 * (t & 7)));
+        if ((t & 7) == 0) eqbm[(KG_TK_T * i + t) >> 3] = ne;
+      }
+    }
+  };
+  if (!MULTI) {
+    load(0);
+    for (int i = t; i < KG_TK_HIST; i += KG_TK_T) lds[i] = 0;     // the first pass's histogram
+  }
 
   // smallest and largest valid key: the bits above their first difference are common to every candidate
   u32 kmin = 0xffffffffu, kmax = 0u;
-  for (int seg = 0; seg < nseg; ++seg) {
-    if (MULTI) load(seg);
-#pragma unroll
-    for (int j = 0; j < KG_TK_V; ++j) kmin = min(kmin, key[j] ? key[j] : 0xffffffffu), kmax = max(kmax, key[j]);
-  }
+  feed_regs([&](u32 k) { kmin = min(kmin, k ? k : 0xffffffffu), kmax = max(kmax, k); });
 #pragma unroll
   for (int o = 32; o; o >>= 1) {
     kmin = min(kmin, (u32)__shfl_xor((int)kmin, o, 64));
@@ -124,85 +273,125 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < KG_TK_T / 64; ++i) kmin = min(kmin, red[0][i]), kmax = max(kmax, red[1][i]);
+  __syncthreads();                                // red is read (its first word becomes the list counter)
+  if (t == 0) red[0][0] = 0;
   const u32 diff = kmin ^ kmax;
   int s = diff ? 32 - __builtin_clz(diff) : 0;   // low bits still to resolve
   u32 m = s >= 32 ? 0u : (0xffffffffu << s);      // the resolved bits
   u32 pm = kmax & m;                              // the threshold's resolved bits
   int need = topk;                                // elements still to take among the candidates
+  int cnt = len;                                  // candidates (elements matching pm on m)
 
-  while (s > 0) {
-    const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
-    for (int i = t; i < 4 * NB; i += KG_TK_T) lds[i] = 0;
-    __syncthreads();
-    for (int seg = 0; seg < nseg; ++seg) {
-      if (MULTI) load(seg);
+  if constexpr (!MULTI) {
+    if (s > 0) {
+      // first pass on the registers; the histogram was cleared before the min / max barrier
+      const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
+      const u32 m0 = m, pm0 = pm;
 #pragma unroll
       for (int j = 0; j < KG_TK_V; ++j) {
-        const int slot = (key[j] & m) == pm ? (int)((((key[j] >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
-                                            : KG_TK_LDS + lane;
-        __hip_atomic_fetch_add(&lds[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const u32 k = key[j];
+        const int slot = (k & m0) == pm0 ? (int)((((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
+                                         : KG_TK_HIST + lane;
+        __hip_atomic_fetch_add(&lds[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
+      __syncthreads();
+      if (w == 0) {
+        int b, ab, c;
+        kg_tk_wave_find<4>(lds, NB, need, b, ab, c);
+        if (lane == 0) found[0] = b, found[1] = ab, found[2] = c;
+      }
+      __syncthreads();
+      need -= found[1];
+      cnt = found[2];
+      pm |= (u32)found[0] << s2;
+      m = 0xffffffffu << s2;
+      s = s2;
+      __syncthreads();                            // found and the histogram are read
     }
-    __syncthreads();
-    // descending bins: thread t sums bins NB-1-2t and NB-2-2t (NB is even)
-    int hh = 0, hl = 0;
-    if (2 * t < NB) {
-      const int4 a = *reinterpret_cast<const int4*>(&lds[(NB - 1 - 2 * t) << 2]);
-      const int4 b = *reinterpret_cast<const int4*>(&lds[(NB - 2 - 2 * t) << 2]);
-      hh = (a.x + a.y) + (a.z + a.w);
-      hl = (b.x + b.y) + (b.z + b.w);
+    if (cnt == need || s == 0 || cnt > KG_TK_CAND) {
+      // resolved by the first pass (or too many candidates to compact: finish on the registers)
+      while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+      const bool ties = cnt > need;
+      __syncthreads();
+      mark(m, pm, !ties, ties);
+      int eq_base = 0, out_base = 0;
+      kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, 0, lo);
+      return;
     }
-    int tot;
-    const int above = kg_tk_scan(hh + hl, wsum, tot);
-    if (2 * t < NB) {
-      if (above < need && need <= above + hh) found[0] = NB - 1 - 2 * t, found[1] = above, found[2] = hh;
-      else if (above + hh < need && need <= above + hh + hl) found[0] = NB - 2 - 2 * t, found[1] = above + hh, found[2] = hl;
-    }
-    __syncthreads();
-    const int b = found[0], ab = found[1], cnt = found[2];
-    __syncthreads();
-    need -= ab;
-    pm |= (u32)b << s2;
-    m = 0xffffffffu << s2;
-    s = s2;
-    if (cnt == need) break;                       // uniform: every element of the bin is taken
-  }
-
-  // Output in index order: an element above the threshold's bits is taken; one equal to them is taken while
-  // fewer than `need` equal ones precede it.  Its position = taken elements of smaller index.  Indices go to
-  // their positions in LDS (the others to a dummy slot), then out coalesced.
-  int above_base = 0, eq_base = 0;
-  for (int seg = 0; seg < nseg; ++seg) {
-    if (MULTI) load(seg);
-    int na = 0, ne = 0;
+    // elements above the bin are taken; the bin's are appended to the list (key, element index) at an LDS
+    // counter, then the registers die
+    int nc = 0;
 #pragma unroll
-    for (int j = 0; j < KG_TK_V; ++j) {
-      na += (key[j] & m) > pm ? 1 : 0;
-      ne += (key[j] & m) == pm ? 1 : 0;
-    }
-    int ta, te;
-    const int pa = kg_tk_scan(na, wsum, ta) + above_base;
-    int pe = kg_tk_scan(ne, wsum, te) + eq_base;
-    int pos = pa + min(pe, need);
-    const int e0 = seg * KG_TK_SEG + t * KG_TK_V - lo;     // indices relative to the row start
+    for (int j = 0; j < KG_TK_V; ++j) nc += (key[j] & m) == pm ? 1 : 0;
+    int pos = nc ? (int)__hip_atomic_fetch_add(&red[0][0], (u32)nc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                 : 0;
+    mark(m, pm, false, false);
 #pragma unroll
-    for (int j = 0; j < KG_TK_V; ++j) {
-      const u32 kk = key[j] & m;
-      const bool take = kk > pm || (kk == pm && pe < need);
-      pe += kk == pm ? 1 : 0;
-      lds[take ? pos : KG_TK_LDS + lane] = e0 + j;
-      pos += take ? 1 : 0;
+    for (int j = 0; j < KG_TK_V; ++j)
+      if ((key[j] & m) == pm) {
+        ckey[pos] = key[j];
+        cidx[pos] = 4 * (KG_TK_T * (j >> 2) + t) + (j & 3);
+        ++pos;
+      }
+    for (int i = t; i < 2048; i += KG_TK_T) eqbm[i] = 0;
+    __syncthreads();
+    // the remaining passes and the list's marks on one wave (LDS operations of a wave complete in order;
+    // the explicit waits only keep the compiler from reordering them)
+    if (w == 0) {
+      const int nl = cnt;                         // list entries: the first pass's bin
+      u32* const h1 = lds + 4096;                 // a one-copy histogram beyond the two bitmaps
+      int c = nl;
+      do {
+        const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
+        for (int i = lane; i < NB; i += 64) h1[i] = 0;
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        const u32 m0 = m, pm0 = pm;
+        for (int i = lane; i < nl; i += 64) {
+          const u32 k = ckey[i];
+          if ((k & m0) == pm0)
+            __hip_atomic_fetch_add(&h1[(k >> s2) & (u32)(NB - 1)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        int b, ab;
+        kg_tk_wave_find<1>(h1, NB, need, b, ab, c);
+        need -= ab;
+        pm |= (u32)b << s2;
+        m = 0xffffffffu << s2;
+        s = s2;
+      } while (c != need && s > 0);
+      // every list entry is above, equal to or below the threshold's bits now
+      const bool ties = c > need;
+      for (int i = lane; i < nl; i += 64) {
+        const u32 kk = ckey[i] & m;
+        const int e = cidx[i];
+        if (kk > pm || (!ties && kk == pm))
+          __hip_atomic_fetch_or(&taken[e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else if (kk == pm)
+          __hip_atomic_fetch_or(&eqbm[e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      if (lane == 0) found[0] = need, found[1] = ties;
     }
-    above_base += ta;
-    eq_base += te;
+    __syncthreads();
+    need = found[0];
+    const bool ties = found[1] != 0;
+    int eq_base = 0, out_base = 0;
+    kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, 0, lo);
+  } else {
+    while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    const bool ties = cnt > need;
+    int eq_base = 0, out_base = 0;
+    for (int seg = 0; seg < nseg; ++seg) {
+      load(seg);
+      __syncthreads();                            // the previous segment's bitmaps are read
+      mark(m, pm, !ties, ties);
+      kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, seg, lo);
+    }
   }
-  __syncthreads();
-  for (int i = t; i < topk; i += KG_TK_T) orow[i] = lds[i];
 }
 
 extern "C" int kg_topk_prefill(const float* logits, const int* starts, const int* ends, int* out, int num_rows,
                                int stride0, int stride1, int topk, int offset, void* stream) {
-  KG_CHECK(logits && starts && ends && out && num_rows >= 0 && offset >= 0 && topk >= 1 && topk <= KG_TK_LDS &&
+  KG_CHECK(logits && starts && ends && out && num_rows >= 0 && offset >= 0 && topk >= 1 &&
            stride1 == 1);
   KG_CHECK(stride0 >= 0 && stride0 % 4 == 0 && kg_aligned(logits, 16));
   if (num_rows == 0) return 0;
