@@ -227,6 +227,57 @@ def producer_launches(data, dev):
     ]
 
 
+def moe_block_measure(data, dev, stream, iters=3):
+    """The whole MoE block (kern_glm53_amd.moe, scripts/gen.py:435-448) at T = 16384: the router GEMM on the bench's
+    activation, routing shaped Zipf-like by the router's score-correction bias (-0.25 ln(1 + rank) over a random
+    expert ranking), the bench's expert weights, a synthetic shared expert.  Returns the mean wall time of the
+    block and of each step (HIP events on the launch stream)."""
+    from kern_glm53_amd import moe, ops, synth
+
+    g = synth.generator(902, "cuda")
+    xn, xq, xsf = data["x_h"], data["xq_h"], data["xsf_h"]
+    ops.quant(xn, H, xq, xsf, M, H, M)
+    rank = torch.randperm(EXPERTS, generator=torch.Generator().manual_seed(903)).float().to(dev)
+    m = data["moe"]
+    sw = {}
+    for name, (n, k, seed) in {"sgu": (2 * INTER, H, 904), "sdn": (H, INTER, 905)}.items():
+        w8, s8 = synth.weights(n, k, synth.generator(seed, "cuda"), device=dev)
+        wq = torch.empty(n, k, dtype=torch.uint8, device=dev)
+        sf = torch.empty(ops.sf_words(k) * n * 4, dtype=torch.uint8, device=dev)
+        ops.requant(w8, s8, wq, sf, n, k, (n + 127) // 128 * 128, 0, 0, n, 0)
+        sw[name] = (wq, sf)
+    W = moe.MoEWeights((torch.randn(EXPERTS, H, generator=g, device=dev) * 0.02).to(torch.bfloat16),
+                       -0.25 * torch.log1p(rank), torch.tensor([2.5], dtype=torch.bfloat16, device=dev),
+                       m["w13"], m["sf13"], m["w2"], m["sf2"], *sw["sgu"], *sw["sdn"])
+    B = moe.MoEBuffers(M, M, dev)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    moe.moe_block(xn, xq, xsf, W, B, out)
+    torch.cuda.synchronize()
+    steps = {}
+    ends = []
+
+    def after(step):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(stream)
+        ends.append((step, e))
+
+    for _ in range(iters):
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        ends.clear()
+        moe.moe_block(xn, xq, xsf, W, B, out, after=after)
+        torch.cuda.synchronize()
+        prev = start
+        for step, e in ends:
+            steps[step] = steps.get(step, 0.0) + prev.elapsed_time(e) / iters
+            prev = e
+    counts = B.counts[:EXPERTS].cpu()
+    res = {"ms": round(sum(steps.values()), 4), "steps_ms": {k: round(v, 4) for k, v in steps.items()},
+           "routed_rows": int(counts.sum()), "expert_rows_min_max": [int(counts.min()), int(counts.max())]}
+    del B, out, W
+    return res
+
+
 def aux_prepare(data, dev):
     """Operands of the absorbed-MLA batched GEMMs and the indexer's MQA logits at the M = 16384 chunk of one
     65536-token sequence (scripts/gen.py:136-139, 178-179, 376, 382-387, 401)."""
@@ -258,6 +309,10 @@ def aux_prepare(data, dev):
     aux["ctx"] = ctx
     aux["klen"] = sum(range(ctx - M + 1, ctx + 1))
     aux["klen_t"] = aux["ke"] - aux["ks"]
+    aux["xn"] = data["x_h"]
+    aux["w_r"], aux["w_p"] = bf(256, H), bf(32, H)
+    aux["rl"] = torch.empty(M, 256, dtype=torch.float32, device=dev)
+    aux["iw"] = torch.empty(M, 32, dtype=torch.bfloat16, device=dev)
     aux["ind"] = torch.empty(M, 2048, dtype=torch.int32, device=dev)
     return aux
 
@@ -279,6 +334,11 @@ def aux_launches(aux):
         ("mqa_logits", lambda: ops.mqa_logits(aux["iq"], aux["kg"], aux["ksf"], aux["w"], aux["ks"], aux["ke"],
                                               aux["logits"], M, ctx, ctx),
          2.0 * 128 * 32 * klen, 4 * klen + M * 32 * 128 + ctx * 132 + M * 136, "mfma"),
+        # the library GEMMs of the layer: the MoE router (f32 out) and the indexer's head weights (bf16 out)
+        ("router_gemm_f32", lambda: ops.gemm_f32(aux["xn"], aux["w_r"], aux["rl"], M, 256, H, 256),
+         2.0 * M * 256 * H, M * H * 2 + 256 * H * 2 + M * 256 * 4, "hbm"),
+        ("weights_proj_gemm_bf16", lambda: ops.gemm_bf16(aux["xn"], aux["w_p"], aux["iw"], M, 32, H, 32),
+         2.0 * M * 32 * H, M * H * 2 + 32 * H * 2 + M * 32 * 2, "hbm"),
         # the indexer's consumer of those logits: read every compressed row once, write 2048 indices a row
         ("topk_prefill", lambda: ops.topk_prefill(aux["logits"], aux["ks"], aux["klen_t"], aux["ind"], M, ctx),
          0.0, 4 * klen + M * 2048 * 4 + M * 8, "hbm"),
@@ -403,6 +463,8 @@ def main():
                            "frac_hbm": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4)}
     del pbufs
     log("producers (us): " + ", ".join(f"{k} {v['us']} ({v['gbps']} GB/s)" for k, v in producers.items()))
+    block = moe_block_measure(data, dev, stream)
+    log(f"moe block: {block['ms']:.3f} ms, " + ", ".join(f"{k} {v:.3f}" for k, v in block["steps_ms"].items()))
     aux = {}
     aux_data = aux_prepare(data, dev)
     for name, fn, flops, nbytes, bound in aux_launches(aux_data):
@@ -433,6 +495,7 @@ def main():
         "kernels": per,
         "glue": glue,
         "producers": producers,
+        "moe_block": block,
         "aux": aux,
     }
     print(json.dumps(line), flush=True)

@@ -22,6 +22,8 @@ SIGNATURES = {
     "kg_fp8_gemm_psum_silu_quant": [P, P, P, P, P, I, I, I, I, I, I, P, P, I, P],
     "kg_bf16_batched": [P, P, P, I, I, I, I, I, LL, LL, LL, LL, LL, LL, P],
     "kg_mqa_logits": [P, P, P, P, P, P, P, I, I, I, P],
+    "kg_gemm_bf16": [P, P, P, I, I, I, I, P],
+    "kg_gemm_bf16_f32": [P, P, P, I, I, I, I, P],
     "kg_quant": [P, I, P, P, I, I, I, P],
     "kg_silu_mul_quant": [P, I, P, P, I, P, I, P],
     "kg_moe_routing": [P, I, I, I, I, P, P, P, P, P, P, P, P],

@@ -45,6 +45,8 @@ KG_DEV v8bf kg_lds_bf16x8(const u8* p) {
   return r;
 }
 
+// F32OUT: the accumulators are stored as f32 (the cuBLAS f32-output GEMM the router uses) instead of bf16.
+template <bool F32OUT>
 __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Args p) {
   constexpr int BM = 128, BN = 128, TI = 2, TJ = 2, SA = BM * 128, STAGE = (BM + BN) * 128;
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
@@ -124,6 +126,28 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
   }
   kg_mfma_drain();
 
+  if constexpr (F32OUT) {
+    // f32 out: lane (lane & 31, lane >> 5) holds columns 8 c + 4 (lane >> 5) .. + 3 of row 32 j + (lane & 31)
+    // of its wave's 64 x 64 quarter, c = 4 i + rr: one 16-byte store each (the f32 outputs here are small).
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int r = m0 + wm * (BM / 2) + j * 32 + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int dn = n0 + wn * (BN / 2) + (i * 4 + rr) * 8 + (lane >> 5) * 4;
+          if (r < p.m && dn < p.n) {
+            float4 o;
+            o.x = acc[i][j][rr * 4 + 0], o.y = acc[i][j][rr * 4 + 1], o.z = acc[i][j][rr * 4 + 2];
+            o.w = acc[i][j][rr * 4 + 3];
+            *reinterpret_cast<float4*>(p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs + 4 * dn) = o;
+          }
+        }
+    }
+    return;
+  }
+
   // Epilogue through LDS: each wave stages its 64 x 64 outputs (rows m, 128-byte rows, 16-byte chunk c in
   // slot c ^ (m & 7)) in the stage (free: the K loop ends with a barrier), then stores 16 bytes per lane,
   // 8 lanes per row: the 128-byte row pieces of D are whole cache lines (D's byte strides are multiples of
@@ -154,9 +178,9 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
   }
 }
 
-extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
-                               long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
-                               long long d_hs, void* stream) {
+static int kg_bf16_launch(bool f32out, const void* a, const void* b, void* d, int m, int n, int k, int rows,
+                          int heads, long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
+                          long long d_hs, void* stream) {
   KG_CHECK(a && b && d && m >= 0 && m <= rows && n > 0 && n % 8 == 0 && k > 0 && k % 64 == 0 && heads > 0);
   KG_CHECK(a_rs % 16 == 0 && a_hs % 16 == 0 && b_rs % 16 == 0 && b_hs % 16 == 0 && d_rs % 16 == 0 &&
            d_hs % 16 == 0);
@@ -170,6 +194,27 @@ extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int
   p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
   const long long total = (long long)heads * p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
-  hipLaunchKernelGGL(kg_bf16_batched_kernel, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
+  if (f32out)
+    hipLaunchKernelGGL(kg_bf16_batched_kernel<true>, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(kg_bf16_batched_kernel<false>, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
+}
+
+extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
+                               long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
+                               long long d_hs, void* stream) {
+  return kg_bf16_launch(false, a, b, d, m, n, k, rows, heads, a_rs, a_hs, b_rs, b_hs, d_rs, d_hs, stream);
+}
+
+// The manifest's library GEMMs (scripts/gen.py:99-102): C[0:m][0:n] = A[m][k] . B[n][k]^T, A and B bf16 row-major
+// with k elements a row, f32 accumulation; C bf16 (gemm_bf16) or f32 (gemm_f32) with ldc elements a row.  One
+// head of the batched kernel.
+extern "C" int kg_gemm_bf16(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream) {
+  KG_CHECK(ldc >= n && ldc % 8 == 0);
+  return kg_bf16_launch(false, a, b, c, m, n, k, m, 1, 2ll * k, 0, 2ll * k, 0, 2ll * ldc, 0, stream);
+}
+extern "C" int kg_gemm_bf16_f32(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream) {
+  KG_CHECK(ldc >= n && ldc % 4 == 0);
+  return kg_bf16_launch(true, a, b, c, m, n, k, m, 1, 2ll * k, 0, 2ll * k, 0, 4ll * ldc, 0, stream);
 }

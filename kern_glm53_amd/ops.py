@@ -14,7 +14,8 @@ import torch
 from ._lib import call
 
 __all__ = [
-    "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "bf16_batched", "mqa_logits", "quant",
+    "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "bf16_batched", "gemm_bf16", "gemm_f32", "mqa_logits",
+    "quant",
     "silu_mul_quant", "routing", "moe_psum", "moe_gather", "moe_combine", "router_topk", "requant", "kvb",
     "add_rms_quant", "mla_prep", "q_post", "topk_prefill", "topk_stream", "topk_slots", "idx_gather", "kv_dequant",
     "sf_words", "counts_len", "EXPERTS", "TOPK", "TILE",
@@ -75,6 +76,16 @@ def bf16_batched(a, b, d, m: int, *, n: int, k: int, rows: int, a_strides, b_str
     with each operand's byte strides (row, head) as in the reference."""
     call("kg_bf16_batched", _ptr(a), _ptr(b), _ptr(d), m, n, k, rows, heads, int(a_strides[0]), int(a_strides[1]),
          int(b_strides[0]), int(b_strides[1]), int(d_strides[0]), int(d_strides[1]), _stream())
+
+
+def gemm_bf16(a, b, c, m: int, n: int, k: int, ldc: int):
+    """The manifest's `gemm_bf16` (scripts/gen.py:99-100): C[:m, :n] = A . B^T in bf16, f32 accumulation."""
+    call("kg_gemm_bf16", _ptr(a), _ptr(b), _ptr(c), m, n, k, ldc, _stream())
+
+
+def gemm_f32(a, b, c, m: int, n: int, k: int, ldc: int):
+    """The manifest's `gemm_f32` (scripts/gen.py:101-102): C[:m, :n] = A . B^T with bf16 inputs, f32 out."""
+    call("kg_gemm_bf16_f32", _ptr(a), _ptr(b), _ptr(c), m, n, k, ldc, _stream())
 
 
 def mqa_logits(iq, kg, ksf, w, ks, ke, logits, num_q: int, num_kv: int, stride: int):

@@ -91,6 +91,9 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     # requant: K % 128, group_rows % 128
     ("kg_requant", [FAKE, FAKE, FAKE, FAKE, 256, 100, 256, 0, 0, 256, 0, NULL]),
     ("kg_requant", [FAKE, FAKE, FAKE, FAKE, 256, 128, 100, 0, 0, 256, 0, NULL]),
+    # library GEMMs: k % 64, ldc < n
+    ("kg_gemm_bf16", [FAKE, FAKE, FAKE, 16, 32, 100, 32, NULL]),
+    ("kg_gemm_bf16_f32", [FAKE, FAKE, FAKE, 16, 256, 6144, 128, NULL]),
     # mqa: negative sizes
     ("kg_mqa_logits", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, 16, 256, NULL]),
     # add_rms_quant: T > sf_rows, q without sf

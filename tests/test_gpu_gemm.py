@@ -244,6 +244,29 @@ def test_bf16_batched_contiguous_k128():
     bf16_ref_check(h(D, np.uint16), A, B, 128, "k128")
 
 
+@pytest.mark.parametrize("m,n,k,ldc", [(1000, 256, 6144, 256), (333, 32, 6144, 40), (16, 264, 192, 272)])
+def test_gemm_f32_and_bf16(m, n, k, ldc):
+    """The manifest's library GEMMs (scripts/gen.py:99-102): the MoE router's f32-output one (gen.py:435) and the
+    indexer's bf16 weights_proj (gen.py:368), C = A . B^T; columns past n of each ldc row untouched."""
+    g = synth.generator(m + n)
+    A = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    B = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    ref32 = A.cpu().float() @ B.cpu().float().T
+    S = A.cpu().float().abs() @ B.cpu().float().abs().T
+    C32 = torch.full((m, ldc), -7.0, dtype=torch.float32, device=DEV)
+    ops.gemm_f32(A, B, C32, m, n, k, ldc)
+    got = C32.cpu()
+    assert bool((got[:, n:] == -7.0).all())
+    assert bool(((got[:, :n] - ref32).abs() <= (k / 16 + 32) * 2.0 ** -24 * S).all())
+    C16 = filled((m, ldc), SENTINEL, torch.int16)
+    ops.gemm_bf16(A, B, C16, m, n, k, ldc)
+    D = h(C16, np.uint16)
+    assert np.all(D[:, n:] == SENTINEL)
+    out = torch.from_numpy(np.ascontiguousarray(D[:, :n]).view(np.int16)).view(torch.bfloat16).float()
+    ok, rel, ratio = ref.check_bf16_gemm(out, ref32, S, k, steps_per_mfma=16)
+    assert ok, f"rel-L2 {rel:.3e}, worst error / tolerance {ratio:.3f}"
+
+
 # ------------------------------------------------------------------ MQA logits (a5)
 
 def mqa_case(num_q, num_kv, seed):
