@@ -25,7 +25,7 @@ struct KgBf16Args {
   const u8* b;
   u8* d;
   long long a_rs, a_hs, b_rs, b_hs, d_rs, d_hs;
-  int m, n, k, heads, m_tiles, n_tiles;
+  int m, n, k, heads, m_tiles, n_tiles, hg;
 };
 
 KG_DEV __amdgpu_buffer_rsrc_t kg_rsrc_b(const void* base, long long bytes) {
@@ -55,9 +55,14 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int wid = kg_xcd_remap_b((int)blockIdx.x, (int)gridDim.x);
-  const int per_head = p.m_tiles * p.n_tiles;
-  const int h = wid / per_head, rest = wid - h * per_head;
-  const int mt = rest / p.n_tiles, nt = rest - mt * p.n_tiles;
+  // Tile order: groups of hg heads (one group per XCD at 64 heads), row-tile major inside a group, so the
+  // workgroups in flight cover whole runs of a row's heads: A's and D's rows are [heads][...] segments
+  // that then stream as long contiguous runs instead of one head's short pieces at a row stride.
+  const int per_row = p.hg * p.n_tiles, per_group = p.m_tiles * per_row;
+  const int g = wid / per_group, rest0 = wid - g * per_group;
+  const int mt = rest0 / per_row, rest = rest0 - mt * per_row;
+  const int hl = rest / p.n_tiles, nt = rest - hl * p.n_tiles;
+  const int h = g * p.hg + hl;
   const int m0 = mt * BM, n0 = nt * BN;
   const int mv = min(BM, p.m - m0), nv = min(BN, p.n - n0);
 
@@ -192,6 +197,7 @@ static int kg_bf16_launch(bool f32out, const void* a, const void* b, void* d, in
   p.a_rs = a_rs, p.a_hs = a_hs, p.b_rs = b_rs, p.b_hs = b_hs, p.d_rs = d_rs, p.d_hs = d_hs;
   p.m = m, p.n = n, p.k = k, p.heads = heads;
   p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
+  p.hg = heads % 8 == 0 ? heads / 8 : heads;
   const long long total = (long long)heads * p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
   if (f32out)

@@ -156,12 +156,18 @@ def test_fp8_gemm_psum_groups(groups, seed):
     assert np.all(out[~owned] == SENTINEL)
 
 
-def test_fp8_gemm_psum_silu_quant_matches_unfused_chain():
+@pytest.mark.parametrize("wide", [False, True])
+def test_fp8_gemm_psum_silu_quant_matches_unfused_chain(wide):
     """The fused epilogue equals gate_up (bf16) followed by glm_silu_mul_quant bit for bit on every live row,
-    and leaves rows no expert owns untouched."""
+    and leaves rows no expert owns untouched.  `wide` gives each row its own activation scale, 2^-30 .. 2^10,
+    so the gate values run from below 2^-13 to above 2^7 (exp(-g) underflowing, overflowing and in range)."""
     T, n, k = 256, 512, 1024
     I = n // 2
     counts, psum, rows, a, sfa, w, sfb = grouped_case(T, n, k, seed=31)
+    if wide:
+        e = np.random.default_rng(32).integers(97, 138, rows).astype(np.uint8)
+        v = sfa.reshape(-1, rows, 4)
+        v[:] = e[None, :, None]
     da, dw, dsfa, dsfb, dpsum = d(a), d(w), d(sfa), d(sfb), d(psum)
     g13 = filled((rows, n), 0, torch.int16)
     ops.fp8_gemm_psum(da, dw, dsfa, dsfb, g13, dpsum, n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows)
@@ -183,6 +189,11 @@ def test_fp8_gemm_psum_silu_quant_matches_unfused_chain():
     W2 = h(sf2, np.uint32).reshape(-1, rows)
     assert np.array_equal(W1[:, owned], W2[:, owned])
     assert np.all(W2[:, ~owned] == 0x5d5d5d5d)
+    if wide:
+        g = h(g13, np.uint16)[owned][:, :I]
+        ex = (g >> 7) & 0xff
+        assert (ex >= 134).any() and ((ex < 114) & ((g & 0x7fff) != 0)).any() and ((ex >= 114) & (ex < 134)).any()
+        return
     # and against the oracle's SiLU-quant of bf16(reference GEMM): equal except where the bf16 rounding of
     # the accumulation-order-dependent f32 sum differs
     ref32, _ = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, 256, n, k, rows, k, rows)
