@@ -24,13 +24,12 @@
 // Selection is a radix select over the order-preserving key of the f32 bits (larger float, larger key;
 // -0 below +0, as the reference's bit transform orders them).  Valid keys are clamped to at least 1 (only a
 // NaN pattern maps to 0) and padding elements get key 0: they sort below every valid element, so they are
-// never taken and never move the threshold, and no pass tests validity.  The bits below the common prefix
-// of the row's smallest and largest valid keys are resolved at most 11 at a time: each pass histograms the
-// candidates' next bits (four interleaved copies, lane & 3, spreading a hot bin's atomics over four banks;
-// non-candidates add to a per-lane dummy slot, so the loop has no branches), then a block-wide suffix scan
-// finds the bin holding the K-th largest.  After the first pass the bin's elements (when at most 8192) are
-// compacted into an LDS list, over which the later passes run.  A pass ends the search early when its bin
-// holds exactly the elements still needed.
+// never taken and never move the threshold, and no pass tests validity.  The key's bits are resolved at
+// most 11 at a time, from the top (below the common prefix of the smallest and largest valid keys for
+// re-read segments): each pass histograms the candidates' next bits (four interleaved copies, lane & 3,
+// spreading a hot bin's atomics over four banks; non-candidates are masked off), then a block-wide suffix
+// scan finds the bin holding the K-th largest.  A pass ends the search early when its bin holds exactly
+// the elements still needed.
 //
 // Output: the K selected indices (relative to the row start) in ascending order, ties at the threshold
 // broken toward the smallest index.  Taken elements set their bit in a 65536-bit LDS bitmap (8 lanes hold
@@ -43,7 +42,6 @@
 #define KG_TK_V 64
 #define KG_TK_SEG (KG_TK_T * KG_TK_V)
 #define KG_TK_HIST 8192                // histogram copies (4 x 2048); then the two bitmaps (2 x 2048 words)
-#define KG_TK_CAND 8192                // candidate list after the first pass
 
 KG_DEV u32 kg_okey(float f) {
   const u32 b = kg_f2u(f);
@@ -92,9 +90,9 @@ KG_DEV void kg_tk_pass(Feed feed, u32* lds, int* wsum, int* found, u32& pm, u32&
   __syncthreads();
   const u32 m0 = m, pm0 = pm;
   feed([&](u32 k) {
-    const int slot = (k & m0) == pm0 ? (int)((((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
-                                     : KG_TK_HIST + lane;
-    __hip_atomic_fetch_add(&lds[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if ((k & m0) == pm0)
+      __hip_atomic_fetch_add(&lds[(((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3)], 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
   });
   __syncthreads();
   // descending bins: thread t sums bins NB-1-2t and NB-2-2t (NB is even)
@@ -145,55 +143,14 @@ KG_DEV void kg_tk_emit(u32* taken, u32* eqbm, bool ties, int need, int& eq_base,
   out_base += tt;
 }
 
-// On one wave: the bin of the need-th largest element among NB bins (bin b's count is the sum of its
-// COPIES words, interleaved).  Lane L takes NB / 64 bins from the top (one bin, or none, when NB < 64), an
-// exclusive scan over lanes finds the lane holding the need-th, which walks its bins.  Wave-uniform results.
-template <int COPIES>
-KG_DEV void kg_tk_wave_find(const u32* hist, int NB, int need, int& bin, int& above, int& cnt) {
-  const int lane = threadIdx.x & 63;
-  const int per = NB >= 64 ? NB / 64 : 1, top = NB - 1 - per * lane;
-  auto count = [&](int b) {
-    u32 c = 0;
-#pragma unroll
-    for (int k = 0; k < COPIES; ++k) c += hist[b * COPIES + k];
-    return (int)c;
-  };
-  int local = 0;
-  if (top >= 0)
-    for (int k = 0; k < per; ++k) local += count(top - k);
-  int inc = local;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int x = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += x;
-  }
-  int b = -1, ab = 0, c = 0;
-  if (inc - local < need && need <= inc) {
-    int run = inc - local;
-    for (int k = 0; k < per; ++k) {
-      const int h = count(top - k);
-      if (run + h >= need) {
-        b = top - k, ab = run, c = h;
-        break;
-      }
-      run += h;
-    }
-  }
-  const int src = __builtin_ctzll(__ballot(b >= 0));
-  bin = __shfl(b, src, 64), above = __shfl(ab, src, 64), cnt = __shfl(c, src, 64);
-}
-
-// MULTI = false: the row (its end within stride0 <= 65536 floats) is held in registers for the first pass,
-// after which the bin's elements are compacted into LDS (key and index) and the registers die; true:
-// segments of 65536 are re-read on every pass (stride0 > 65536).
+// MULTI = false: the row (its end within stride0 <= 65536 floats) is held in registers for every pass;
+// true: segments of 65536 are re-read on every pass (stride0 > 65536).
 template <bool MULTI>
 __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restrict__ logits,
                                                            const int* __restrict__ starts,
                                                            const int* __restrict__ ends, int* __restrict__ out,
                                                            int stride0, int topk, int offset) {
-  __shared__ __attribute__((aligned(16))) u32 lds[KG_TK_HIST + 64];  // + a dummy slot per lane
-  __shared__ u32 ckey[KG_TK_CAND];
-  __shared__ int cidx[KG_TK_CAND];
+  __shared__ __attribute__((aligned(16))) u32 lds[KG_TK_HIST];
   __shared__ int wsum[KG_TK_T / 64];
   __shared__ u32 red[2][KG_TK_T / 64];
   __shared__ int found[3];
@@ -256,124 +213,42 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
       }
     }
   };
-  if (!MULTI) {
-    load(0);
-    for (int i = t; i < KG_TK_HIST; i += KG_TK_T) lds[i] = 0;     // the first pass's histogram
-  }
-
-  // smallest and largest valid key: the bits above their first difference are common to every candidate
-  u32 kmin = 0xffffffffu, kmax = 0u;
-  feed_regs([&](u32 k) { kmin = min(kmin, k ? k : 0xffffffffu), kmax = max(kmax, k); });
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    kmin = min(kmin, (u32)__shfl_xor((int)kmin, o, 64));
-    kmax = max(kmax, (u32)__shfl_xor((int)kmax, o, 64));
-  }
-  if (lane == 0) red[0][w] = kmin, red[1][w] = kmax;
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < KG_TK_T / 64; ++i) kmin = min(kmin, red[0][i]), kmax = max(kmax, red[1][i]);
-  __syncthreads();                                // red is read (its first word becomes the list counter)
-  if (t == 0) red[0][0] = 0;
-  const u32 diff = kmin ^ kmax;
-  int s = diff ? 32 - __builtin_clz(diff) : 0;   // low bits still to resolve
-  u32 m = s >= 32 ? 0u : (0xffffffffu << s);      // the resolved bits
-  u32 pm = kmax & m;                              // the threshold's resolved bits
+  int s = 32;                                     // low bits still to resolve
+  u32 m = 0u;                                     // the resolved bits
+  u32 pm = 0u;                                    // the threshold's resolved bits
   int need = topk;                                // elements still to take among the candidates
   int cnt = len;                                  // candidates (elements matching pm on m)
+  if constexpr (MULTI) {
+    // smallest and largest valid key: the bits above their first difference are common to every
+    // candidate, which can save a pass over the re-read segments
+    u32 kmin = 0xffffffffu, kmax = 0u;
+    feed_regs([&](u32 k) { kmin = min(kmin, k ? k : 0xffffffffu), kmax = max(kmax, k); });
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+      kmin = min(kmin, (u32)__shfl_xor((int)kmin, o, 64));
+      kmax = max(kmax, (u32)__shfl_xor((int)kmax, o, 64));
+    }
+    if (lane == 0) red[0][w] = kmin, red[1][w] = kmax;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < KG_TK_T / 64; ++i) kmin = min(kmin, red[0][i]), kmax = max(kmax, red[1][i]);
+    __syncthreads();                              // red is read
+    const u32 diff = kmin ^ kmax;
+    s = diff ? 32 - __builtin_clz(diff) : 0;
+    m = s >= 32 ? 0u : (0xffffffffu << s);
+    pm = kmax & m;
+  }
 
   if constexpr (!MULTI) {
-    if (s > 0) {
-      // first pass on the registers; the histogram was cleared before the min / max barrier
-      const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
-      const u32 m0 = m, pm0 = pm;
-#pragma unroll
-      for (int j = 0; j < KG_TK_V; ++j) {
-        const u32 k = key[j];
-        const int slot = (k & m0) == pm0 ? (int)((((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3))
-                                         : KG_TK_HIST + lane;
-        __hip_atomic_fetch_add(&lds[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-      __syncthreads();
-      if (w == 0) {
-        int b, ab, c;
-        kg_tk_wave_find<4>(lds, NB, need, b, ab, c);
-        if (lane == 0) found[0] = b, found[1] = ab, found[2] = c;
-      }
-      __syncthreads();
-      need -= found[1];
-      cnt = found[2];
-      pm |= (u32)found[0] << s2;
-      m = 0xffffffffu << s2;
-      s = s2;
-      __syncthreads();                            // found and the histogram are read
-    }
-    if (cnt == need || s == 0 || cnt > KG_TK_CAND) {
-      // resolved by the first pass (or too many candidates to compact: finish on the registers)
-      while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
-      const bool ties = cnt > need;
-      __syncthreads();
-      mark(m, pm, !ties, ties);
-      int eq_base = 0, out_base = 0;
-      kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, 0, lo);
-      return;
-    }
-    // elements above the bin are taken; the bin's are appended to the list (key, element index) at an LDS
-    // counter, then the registers die
-    int nc = 0;
-#pragma unroll
-    for (int j = 0; j < KG_TK_V; ++j) nc += (key[j] & m) == pm ? 1 : 0;
-    int pos = nc ? (int)__hip_atomic_fetch_add(&red[0][0], (u32)nc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
-                 : 0;
-    mark(m, pm, false, false);
-#pragma unroll
-    for (int j = 0; j < KG_TK_V; ++j)
-      if ((key[j] & m) == pm) {
-        ckey[pos] = key[j];
-        cidx[pos] = 4 * (KG_TK_T * (j >> 2) + t) + (j & 3);
-        ++pos;
-      }
-    for (int i = t; i < 2048; i += KG_TK_T) eqbm[i] = 0;
-    __syncthreads();
-    // the remaining passes and the list's marks on one wave (LDS operations of a wave complete in order;
-    // the explicit waits only keep the compiler from reordering them)
-    if (w == 0) {
-      const int nl = cnt;                         // list entries: the first pass's bin
-      u32* const h1 = lds + 4096;                 // a one-copy histogram beyond the two bitmaps
-      int c = nl;
-      do {
-        const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
-        for (int i = lane; i < NB; i += 64) h1[i] = 0;
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        const u32 m0 = m, pm0 = pm;
-        for (int i = lane; i < nl; i += 64) {
-          const u32 k = ckey[i];
-          if ((k & m0) == pm0)
-            __hip_atomic_fetch_add(&h1[(k >> s2) & (u32)(NB - 1)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        int b, ab;
-        kg_tk_wave_find<1>(h1, NB, need, b, ab, c);
-        need -= ab;
-        pm |= (u32)b << s2;
-        m = 0xffffffffu << s2;
-        s = s2;
-      } while (c != need && s > 0);
-      // every list entry is above, equal to or below the threshold's bits now
-      const bool ties = c > need;
-      for (int i = lane; i < nl; i += 64) {
-        const u32 kk = ckey[i] & m;
-        const int e = cidx[i];
-        if (kk > pm || (!ties && kk == pm))
-          __hip_atomic_fetch_or(&taken[e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        else if (kk == pm)
-          __hip_atomic_fetch_or(&eqbm[e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-      if (lane == 0) found[0] = need, found[1] = ties;
-    }
-    __syncthreads();
-    need = found[0];
-    const bool ties = found[1] != 0;
+    // every pass over the registers, from the top 11 bits down, the first one consuming the keys as their
+    // loads land.  At 16384 rows of 49153-65536 MQA logits this ran 1.43 ms, against 1.74 with a min / max
+    // prologue (the common prefix it finds saves a pass, but the histogram then waits for every load),
+    // 1.9 with the bin found by one wave instead of a block-wide scan, and 2.1 with the first pass's bin
+    // compacted into an LDS list for one wave to finish.
+    load(0);
+    while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    const bool ties = cnt > need;
+    mark(m, pm, !ties, ties);
     int eq_base = 0, out_base = 0;
     kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, 0, lo);
   } else {
