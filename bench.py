@@ -392,8 +392,8 @@ def main():
                     help="only run three device-to-device copies of MIB MiB (calibrates HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path (each GEMM shards trivially by "
-              "rows / experts / heads, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one MI355X: the library has no multi-GPU path (each GEMM shards trivially by "
+              "rows / experts / heads); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     dev = torch.device("cuda:0")

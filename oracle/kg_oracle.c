@@ -1,7 +1,7 @@
 /*
  * TEST INFRASTRUCTURE ONLY.  This file is the oracle: a plain-C, single-threaded restatement of the
  * byte / integer / order-fixed float arithmetic of kern-glm53's `glm_deepgemm` path glue.  Only the test
- * suite, the smoke check and the bench's CPU-baseline leg load it, as the checker; the product library
+ * suite, the smoke check and the bench's CPU-baseline leg load it, to check the product against; the product library
  * (kern_glm53_amd/csrc) never links, calls or falls back to it.
  *
  * Every function cites the reference lines it restates (paths relative to the reference checkout).
@@ -328,7 +328,7 @@ void kgo_kvb(const u8* w, const float* s, u16* kvb, u16* wuk) {
 static inline float rnd_bf16(float x) { return kgo_bf16_to_f32(kgo_f32_to_bf16(x)); }
 
 /* The reference's rsqrtf (a hardware approximation, up to 2 ulp from 1/sqrt on its GPUs) is restated
- * as the correctly rounded quotient 1 / sqrtf(x): both sides of this build evaluate exactly that, and it
+ * as the correctly rounded quotient 1 / sqrtf(x): the oracle and the kernels both evaluate exactly that, and it
  * is within 3 ulp of the reference's value. */
 static inline float rsqrt_rn(float x) { return 1.0f / sqrtf(x); }
 

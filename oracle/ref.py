@@ -1,7 +1,7 @@
 """TEST INFRASTRUCTURE ONLY: the oracle for kern-glm53's `glm_deepgemm` path.
 
-Only the test suite, `__graft_entry__.smoke()` and `bench.py`'s `cpu_baseline` leg import this module, as
-the checker.  The product (`kern_glm53_amd`) never imports, links or falls back to it.
+Only the test suite, `__graft_entry__.smoke()` and `bench.py`'s `cpu_baseline` leg import this module, to
+check the product against.  The product (`kern_glm53_amd`) never imports, links or falls back to it.
 
 Two halves:
   * the byte / integer / order-fixed glue restated in plain C (`kg_oracle.c`, built into

@@ -2,7 +2,7 @@
 float8 cast, closed forms from math.frexp, numpy cumsum / bincount, exact rational arithmetic, brute-force
 loops, and single-nonzero probes that fix every index of the scale layouts.  The reference ships no
 golden vectors for this path; its only known-answer test (fast_div(16), scripts/glm_ops.py:200) belongs
-to the routing kernel's parameter pack, which this build's routing entry point does not use."""
+to the routing kernel's parameter pack, which the library's routing entry point does not use."""
 import math
 from fractions import Fraction
 
