@@ -243,6 +243,22 @@ def test_bf16_batched_uv_layout():
     bf16_ref_check(h(ov, np.uint16), o, B, 512, "uv")
 
 
+def test_bf16_batched_many_tiles():
+    """Many tiles (1500 rows: 12 row tiles x 64 heads x 4 column tiles, more than the CUs hold at once) in the
+    head-group tile order; M tail."""
+    rows, m = 1504, 1500
+    g = synth.generator(44)
+    qb = (torch.randn(rows, 20480, generator=g)).to(torch.bfloat16).to(DEV)
+    wuk = (torch.randn(64, 512, 192, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    qmla = filled((rows, 64, 576), SENTINEL, torch.int16)
+    ops.bf16_batched(qb, wuk, qmla, m, n=512, k=192, rows=rows, a_strides=(40960, 512), b_strides=(384, 196608),
+                     d_strides=(73728, 1152))
+    D = h(qmla, np.uint16)
+    A = qb[:m, :16384].view(m, 64, 256)[:, :, :192]
+    bf16_ref_check(np.ascontiguousarray(D[:m, :, :512]), A, wuk, 192, "uk many tiles")
+    assert np.all(D[:m, :, 512:] == SENTINEL) and np.all(D[m:] == SENTINEL)
+
+
 def test_bf16_batched_contiguous_k128():
     """The configured W_UK shape: 64 heads x [m x 128] . [128 x 512], contiguous operands, M tail."""
     rows, m = 130, 130
@@ -255,7 +271,8 @@ def test_bf16_batched_contiguous_k128():
     bf16_ref_check(h(D, np.uint16), A, B, 128, "k128")
 
 
-@pytest.mark.parametrize("m,n,k,ldc", [(1000, 256, 6144, 256), (333, 32, 6144, 40), (16, 264, 192, 272)])
+@pytest.mark.parametrize("m,n,k,ldc", [(1000, 256, 6144, 256), (333, 32, 6144, 40), (16, 264, 192, 272),
+                                       (40000, 256, 128, 256)])
 def test_gemm_f32_and_bf16(m, n, k, ldc):
     """The manifest's library GEMMs (scripts/gen.py:99-102): the MoE router's f32-output one (gen.py:435) and the
     indexer's bf16 weights_proj (gen.py:368), C = A . B^T; columns past n of each ldc row untouched."""
