@@ -23,7 +23,7 @@ def run_topk(logits, starts, ends, k, num_rows=None, offset=0):
     return got, out_ref
 
 
-@pytest.mark.parametrize("case", ["mixed", "full", "ties", "unaligned", "long", "window", "k256"])
+@pytest.mark.parametrize("case", ["mixed", "full", "ties", "unaligned", "long", "window", "k256", "specials"])
 def test_topk_prefill_bit_exact(case):
     print(f"topk_prefill case={case}", flush=True)
     rng = np.random.default_rng(sum(map(ord, case)))
@@ -41,10 +41,18 @@ def test_topk_prefill_bit_exact(case):
         lens, stride0 = [70000, 131072, 66000, 100], 131072
     elif case == "window":
         lens, stride0 = [5000] * 8, 5120
+    elif case == "specials":
+        lens, stride0 = [5000, 3000, 2100, 70], 5120
     else:
         lens, stride0, k = [300, 256, 257, 9000], 9000, 256
     R = len(lens)
     logits = (rng.standard_normal((R, stride0)) * rng.uniform(0.01, 100, (R, 1))).astype(np.float32)
+    if case == "specials":   # infinities, NaNs of both signs, denormals and zeros, in the reference's bit order
+        special = np.array([0x7f800000, 0xff800000, 0x7fc00000, 0xffc00000, 0x7f800001, 0x00000001, 0x80000001,
+                            0x00000000, 0x80000000, 0x007fffff], np.uint32).view(np.float32)
+        for r in range(R):
+            pos = rng.choice(lens[r], min(lens[r], 400), replace=False)
+            logits[r, pos] = special[rng.integers(0, len(special), len(pos))]
     starts = np.zeros(R, np.int32)
     if case == "ties":
         logits = np.round(logits * 3).astype(np.float32)

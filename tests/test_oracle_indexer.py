@@ -61,6 +61,23 @@ def test_topk_prefill_ties_starts_and_signed_zero():
     assert not np.isin(np.arange(10, 20), out[2]).any()       # the -0 entries lose to the +0 ones
 
 
+def test_topk_prefill_specials_follow_the_bit_order():
+    """Infinities, NaNs of both signs, denormals and signed zeros rank by the reference's bit transform:
+    +NaN above +inf, -NaN below -inf (lexsort over the same key is the independent formulation)."""
+    rng = np.random.default_rng(12)
+    logits = rng.standard_normal((2, 3000)).astype(np.float32)
+    special = np.array([0x7f800000, 0xff800000, 0x7fc00000, 0xffc00000, 0x00000001, 0x80000001, 0, 0x80000000],
+                       np.uint32).view(np.float32)
+    for r in range(2):
+        pos = rng.choice(3000, 300, replace=False)
+        logits[r, pos] = special[rng.integers(0, len(special), 300)]
+    out = ref.topk_prefill(logits, np.zeros(2, np.int32), np.array([3000, 2500], np.int32), 256)
+    for r, n in enumerate([3000, 2500]):
+        assert np.array_equal(out[r], expected_topk(logits[r, :n], 256))
+        nan_pos = np.nonzero(logits[r, :n].view(np.uint32) == 0x7fc00000)[0]
+        assert np.isin(nan_pos, out[r]).all()               # every +NaN is taken (it ranks first)
+
+
 def test_topk_prefill_offset_rows_only():
     logits = np.random.default_rng(6).standard_normal((4, 512)).astype(np.float32)
     out = ref.topk_prefill(logits, np.zeros(4, np.int32), np.full(4, 512, np.int32), 16, num_rows=2, offset=1)
