@@ -77,6 +77,38 @@ def test_fp8_gemm(M, N, K, rows, lda, ldc, sfa_rows):
     assert np.all(out[:M, N:] == SENTINEL) and np.all(out[M:] == SENTINEL)
 
 
+@pytest.mark.parametrize("N,K,ldc", [(2624, 6144, 2752), (16384, 2048, 20480), (6144, 16384, 6144)])
+def test_fp8_gemm_bench_shapes_sampled(N, K, ldc):
+    """The bench's dense GEMMs at full size (M = 16384: q_a/kv_a, q_b, o_proj): activations quantized on the
+    GPU by glm_quant (bit-exact against the oracle elsewhere), random e4m3 weights and UE8M0 scales; 16
+    output rows (tile edges and random ones) against the oracle's dequantize-then-matmul, every column."""
+    M = 16384
+    print(f"fp8 gemm 16384 x {N} x {K}", flush=True)
+    g = synth.generator(N + K, "cuda")
+    x = synth.activations(M, K, g, device="cuda")
+    q = torch.empty(M, K, dtype=torch.uint8, device=DEV)
+    sf = torch.empty(ref.sf_words(K) * M * 4, dtype=torch.uint8, device=DEV)
+    ops.quant(x, K, q, sf, M, K, M)
+    w = torch.randint(0, 256, (N, K), generator=g, device=DEV, dtype=torch.int32)
+    w = torch.where((w & 0x7f) == 0x7f, w ^ 1, w).to(torch.uint8)            # no NaN codes
+    sfb = torch.randint(118, 127, (ref.sf_words(K) * N * 4,), generator=g, device=DEV, dtype=torch.int32)
+    sfb = sfb.to(torch.uint8)
+    c = torch.full((M, ldc), -7.0, dtype=torch.bfloat16, device=DEV)
+    ops.fp8_gemm(q, w, sf, sfb, c, M, n=N, k=K, rows=M, lda=K, ldc=ldc, sfa_rows=M)
+    rows = sorted({0, 1, 255, 256, 8191, 8192, 16127, 16383} |
+                  set(np.random.default_rng(N).choice(M, 8, replace=False).tolist()))
+    R = len(rows)
+    a_s = h(q[rows], np.uint8)
+    sfa_s = np.ascontiguousarray(h(sf, np.uint8).reshape(-1, M, 4)[:, rows, :]).reshape(-1)
+    w_h, sfb_h = h(w, np.uint8), h(sfb, np.uint8)
+    ref32 = ref.fp8_gemm(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
+    S = ref.fp8_gemm_abs(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
+    Wb = ref.fp8_window_bound(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
+    out = h(c.view(torch.int16), np.uint16)
+    check(np.ascontiguousarray(out[rows, :N]), ref32, S, K, f"dense 16384x{N}x{K}", Wb)
+    assert np.all(out[rows, N:] == 0xc0e0)                                     # bf16 -7.0 past n untouched
+
+
 def test_fp8_gemm_scale_linearity():
     """Raising one activation row's exponent bytes by 3 multiplies exactly that output row by 8 (the
     kernel applies the UE8M0 scales exactly)."""
