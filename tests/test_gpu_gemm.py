@@ -362,6 +362,30 @@ def check_mqa(out, q8, k8, ksf, w, ks, ke, stride):
         assert np.all(out[r, n:] == -12345.0), f"row {r} written past its key count"
 
 
+def test_mqa_logits_bench_shape_sampled():
+    """The bench's shape at full size: the last 16384 rows of one 65536-token sequence, causal, random e4m3
+    codes and power-of-two key scales as the bench draws them; 6 rows (the first, the last, random) against
+    the oracle over all their keys, and every row's tail past its key count untouched."""
+    M, ctx = 16384, 65536
+    print("mqa logits 16384 x 65536", flush=True)
+    g = synth.generator(901, "cuda")
+    codes = lambda *s: (torch.randint(0, 0x78, s, generator=g, device=DEV, dtype=torch.int32)
+                        | (torch.randint(0, 2, s, generator=g, device=DEV, dtype=torch.int32) << 7)).to(torch.uint8)
+    iq, kg = codes(M, 32, 128), codes(ctx, 128)
+    ksf = torch.exp2(torch.randint(-8, 0, (ctx,), generator=g, device=DEV).float())
+    w = torch.randn(M, 32, generator=g, device=DEV) * (128 ** -0.5) * (32 ** -0.5)
+    ks = torch.zeros(M, dtype=torch.int32, device=DEV)
+    ke = torch.arange(M, dtype=torch.int32, device=DEV) + (ctx - M) + 1
+    logits = torch.full((M, ctx), -12345.0, dtype=torch.float32, device=DEV)
+    ops.mqa_logits(iq, kg, ksf, w, ks, ke, logits, M, ctx, ctx)
+    tail_ok = torch.arange(ctx, device=DEV)[None, :] < ke[:, None].long()
+    assert bool(((logits == -12345.0) | tail_ok).all())                       # nothing written past ke
+    rows = sorted({0, M - 1} | set(np.random.default_rng(5).choice(M, 4, replace=False).tolist()))
+    out = h(logits[rows], np.float32)
+    check_mqa(out, h(iq[rows], np.uint8), h(kg, np.uint8), h(ksf, np.float32), h(w[rows], np.float32),
+              h(ks[rows], np.int32).astype(np.int64), h(ke[rows], np.int32).astype(np.int64), ctx)
+
+
 def test_mqa_logits_ragged():
     num_q, num_kv, stride = 37, 1000, 1024
     q8, k8, ksf, w = mqa_case(num_q, num_kv, 51)
