@@ -291,6 +291,30 @@ def test_bf16_batched_many_tiles():
     assert np.all(D[:m, :, 512:] == SENTINEL) and np.all(D[m:] == SENTINEL)
 
 
+def test_bf16_batched_bench_shapes_sampled():
+    """W_UK and W_UV at the bench's 16384 rows in the reference's layouts; 8 rows of every head against the
+    oracle."""
+    M = 16384
+    print("bf16 batched 16384 rows x 64 heads (W_UK, W_UV)", flush=True)
+    g = synth.generator(45, "cuda")
+    rows = sorted({0, 127, 128, M - 1} | set(np.random.default_rng(6).choice(M, 4, replace=False).tolist()))
+    qb = torch.randn(M, 20480, generator=g, device=DEV).to(torch.bfloat16)
+    wuk = (torch.randn(64, 512, 192, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    qmla = torch.empty(M, 64, 576, dtype=torch.bfloat16, device=DEV)
+    ops.bf16_batched(qb, wuk, qmla, M, n=512, k=192, rows=M, a_strides=(40960, 512), b_strides=(384, 196608),
+                     d_strides=(73728, 1152))
+    A = qb[rows, :16384].view(len(rows), 64, 256)[:, :, :192].cpu()
+    bf16_ref_check(h(qmla[rows, :, :512].contiguous().view(torch.int16), np.uint16), A, wuk.cpu(), 192, "uk 16384")
+    del qb, qmla
+    o = torch.randn(M, 64, 512, generator=g, device=DEV).to(torch.bfloat16)
+    kvb = (torch.randn(64 * 448, 512, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    ov = torch.empty(M, 64, 256, dtype=torch.bfloat16, device=DEV)
+    ops.bf16_batched(o, kvb.view(-1)[192 * 512:], ov, M, n=256, k=512, rows=M, a_strides=(65536, 1024),
+                     b_strides=(1024, 458752), d_strides=(32768, 512))
+    B = kvb.view(64, 448, 512)[:, 192:448, :].cpu()
+    bf16_ref_check(h(ov[rows].contiguous().view(torch.int16), np.uint16), o[rows].cpu(), B, 512, "uv 16384")
+
+
 def test_bf16_batched_contiguous_k128():
     """The configured W_UK shape: 64 heads x [m x 128] . [128 x 512], contiguous operands, M tail."""
     rows, m = 130, 130
