@@ -171,6 +171,43 @@ def test_combine_bit_exact():
     assert np.array_equal(h(out, np.uint16), want)
 
 
+def test_gather_combine_full_size():
+    """16384 tokens x top-8 (Zipf routing) through the routing tables: every routed row of the gather is its
+    token's row and scale words (all 131072 of them, compared on the GPU), and 16 sampled tokens of the
+    combine against the oracle on their own rows."""
+    T, x_rows = 16384, 16384
+    print("gather / combine 16384 x top-8", flush=True)
+    ids = zipf_ids(T, 21)
+    tab = run_routing(ids)
+    e2p = d(tab["exp2perm"])
+    a_rows = 8 * T + 256 * 128
+    g = synth.generator(22, "cuda")
+    xq = torch.randint(0, 256, (x_rows, 6144), generator=g, device=DEV, dtype=torch.uint8)
+    xsf = torch.randint(-2 ** 31, 2 ** 31 - 1, (12 * x_rows,), generator=g, device=DEV, dtype=torch.int32)
+    aq = filled((a_rows, 6144), 0x11)
+    asf = filled((12 * a_rows,), 0x22222222, torch.int32)
+    ops.moe_gather(xq, xsf, x_rows, e2p, aq, asf, a_rows, T=T)
+    valid = e2p >= 0
+    p = e2p[valid].long()
+    t = torch.arange(T, device=DEV)[:, None].expand(T, 8)[valid]
+    assert int(valid.sum()) == 8 * T
+    assert torch.equal(aq[p], xq[t])
+    assert torch.equal(asf.view(12, a_rows)[:, p], xsf.view(12, x_rows)[:, t])
+    rows = tab["total_padded"]
+    fc2 = torch.randn(rows, 6144, generator=g, device=DEV).to(torch.bfloat16)
+    shared = torch.randn(T, 6144, generator=g, device=DEV).to(torch.bfloat16)
+    wts = torch.rand(T, 8, generator=g, device=DEV)
+    out = torch.empty(T, 6144, dtype=torch.bfloat16, device=DEV)
+    ops.moe_combine(fc2, e2p, wts, shared, out, T)
+    sample = sorted({0, T - 1} | set(np.random.default_rng(23).choice(T, 14, replace=False).tolist()))
+    e2p_h = tab["exp2perm"][sample]
+    fc2_s = h(fc2[torch.from_numpy(np.maximum(e2p_h, 0).reshape(-1)).to(DEV).long()].view(torch.int16), np.uint16)
+    e2p_s = np.where(e2p_h >= 0, np.arange(8 * len(sample)).reshape(-1, 8), -1).astype(np.int32)
+    want = ref.moe_combine(fc2_s, e2p_s, h(wts[sample], np.float32), h(shared[sample].view(torch.int16), np.uint16),
+                           len(sample))
+    assert np.array_equal(h(out[sample].view(torch.int16), np.uint16), want)
+
+
 # ------------------------------------------------------------------ router (a11)
 
 def test_router_topk_bit_exact():
