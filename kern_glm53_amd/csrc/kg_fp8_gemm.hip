@@ -402,7 +402,10 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 // each 32-row MFMA tile j goes through it in two halves of 16 rows (256 bytes each; chunk c of 8 columns
 // of row m in slot c ^ m, which makes both the 8-byte writes of the half's 16 rows and the 16-byte reads
 // conflict-free).  Every wave issues exactly 32 stores per tile, which the next tile's first barrier
-// leaves in flight.
+// leaves in flight.  The stores are non-temporal (the kernel never reads its outputs back; o_proj ran 2.7%
+// faster).  Storing from the registers instead (v_permlane32_swap pairs, 16 bytes per lane, 32 bytes per row
+// per instruction) skipped the staging but ran q_b at 0.86 ms against 0.47: the rows' 256-byte segments
+// matter more than the two LDS round trips per 16 rows.
 KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int m0, int m_end,
                                 int n0, int wm, int wn, bool half) {
   // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
@@ -440,7 +443,7 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
         // resource, which drops the write
         const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
         __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
-        __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 2 /* nt */);
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);         // reads done before the next half's writes
     }
