@@ -398,14 +398,14 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 }
 
 // Epilogue of the persistent kernel for modes 0 and 1: bf16 through LDS, so that each store writes 16
-// contiguous bytes per lane and 16 lanes cover a 256-byte row segment.  `stage` is the wave's own 4 KB:
-// each 32-row MFMA tile j goes through it in two halves of 16 rows (256 bytes each; chunk c of 8 columns
-// of row m in slot c ^ m, which makes both the 8-byte writes of the half's 16 rows and the 16-byte reads
-// conflict-free).  Every wave issues exactly 32 stores per tile, which the next tile's first barrier
-// leaves in flight.  The stores are non-temporal (the kernel never reads its outputs back; o_proj ran 2.7%
-// faster).  Storing from the registers instead (v_permlane32_swap pairs, 16 bytes per lane, 32 bytes per row
-// per instruction) skipped the staging but ran q_b at 0.86 ms against 0.47: the rows' 256-byte segments
-// matter more than the two LDS round trips per 16 rows.
+// contiguous bytes per lane and 8 lanes cover a 128-byte row segment (a whole line).  `stage` is the wave's
+// own 4 KB: each 32-row MFMA tile j goes through it in two rounds of 64 columns (n tiles 2 ch, 2 ch + 1), all
+// 64 lanes writing their rows' 8-byte pieces (chunk c of 8 columns of row m in slot c ^ (m & 7)), then
+// reading 16-byte chunks back.  Every wave issues exactly 32 stores per tile, which the next tile's first
+// barrier leaves in flight.  The stores are non-temporal (the kernel never reads its outputs back; o_proj ran
+// 2.7% faster).  Against rounds of 16 rows x 128 columns (half the lanes writing, 256-byte row segments) this
+// took q_b from 0.465 to 0.451 ms.  Storing from the registers instead (v_permlane32_swap pairs, 32 bytes per
+// row per instruction) skipped the staging but ran q_b at 0.86 ms: whole-line row segments matter most.
 KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int m0, int m_end,
                                 int n0, int wm, int wn, bool half) {
   // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
@@ -414,38 +414,37 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
   const __amdgpu_buffer_rsrc_t rc = kg_rsrc(p.c, (long long)p.rows * p.ldc * 2);
   const int mr = lane & 31;                       // this lane's row of the MFMA tile
-  u8* const wrow = stage + (mr & 15) * 256 + ((lane >> 5) << 3);
+  u8* const wrow = stage + mr * 128 + ((lane >> 5) << 3);
   const int rbase = m0 + (half ? wm * 64 : wm * 128);   // a half tile's waves own 64 rows each
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool jv = !half || j < 2;               // a half tile has two m tiles per wave
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      if (jv && (mr >> 4) == hh) {
+    for (int ch = 0; ch < 2; ++ch) {
+      // the 32 rows x 64 columns (n tiles 2 ch, 2 ch + 1) of m tile j: chunk c = 4 i' + rr of row mr
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+      for (int il = 0; il < 2; ++il)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int c = i * 4 + rr;
-            uint2 o;
-            o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
-            o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
-            *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 15)) << 4)) = o;
-          }
-      }
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = il * 4 + rr, i = 2 * ch + il;
+          uint2 o;
+          o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 7)) << 4)) = o;
+        }
       __builtin_amdgcn_s_waitcnt(0xc07f);         // lgkmcnt(0): this wave's writes are in LDS
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int idx = t * 64 + lane, m = idx >> 4, c = idx & 15;
-        const uint4 v = *reinterpret_cast<const uint4*>(stage + m * 256 + ((c ^ m) << 4));
-        const int gm = rbase + j * 32 + hh * 16 + m, gn = n0 + wn * 128 + c * 8;
+        const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + m * 128 + ((c ^ (m & 7)) << 4));
+        const int gm = rbase + j * 32 + m, gn = n0 + wn * 128 + ch * 64 + c * 8;
         // always issued (no branch); lanes outside the tile's rows or columns get an offset past the
         // resource, which drops the write
         const unsigned off = jv && gm < m_end && gn < p.n ? (unsigned)(gm * p.ldc + gn) * 2u : 0x80000000u;
         __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
         __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 2 /* nt */);
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);         // reads done before the next half's writes
+      __builtin_amdgcn_s_waitcnt(0xc07f);         // reads done before the next round's writes
     }
   }
 }
