@@ -1,0 +1,87 @@
+"""Seeded random shapes through the GEMMs and the prefill top-k, beyond the hand-picked edge cases: dense fp8
+GEMMs on both kernels (the 128 x 128 tile kernel for small or odd-width outputs, the persistent one for at
+least 256 tiles of 256 x 256) with random tails, strides and scale-row counts; grouped GEMMs with random
+expert counts; top-k rows of random lengths, starts and K.  Each case against the oracle, at the same bars
+as the fixed cases (GEMMs within the f32-accumulation and MFMA-window bounds, top-k bit for bit)."""
+import numpy as np
+import pytest
+import torch
+
+from kern_glm53_amd import ops
+from oracle import ref
+from tests._gpu import DEV, d, filled, h
+from tests.test_gpu_gemm import SENTINEL, check, quant_act, quant_weight
+
+pytestmark = pytest.mark.gpu
+
+
+def dense_shapes():
+    rng = np.random.default_rng(2024)
+    out = []
+    for i in range(8):
+        big = i >= 5                                            # the persistent kernel's range
+        M = int(rng.integers(4097, 4700)) if big else int(rng.integers(1, 3000))
+        N = int(rng.integers(4097, 4400)) // 8 * 8 if big else int(rng.integers(1, 1200))
+        K = 128 * int(rng.integers(1, 5 if big else 24))
+        lda = K + 16 * int(rng.integers(0, 4))
+        ldc = (N + 7) // 8 * 8 + 8 * int(rng.integers(0, 3)) if big else (N + 3) // 4 * 4 + 4 * int(rng.integers(0, 3))
+        rows = M + int(rng.integers(0, 40))
+        out.append((M, N, K, rows, lda, ldc, rows + int(rng.integers(0, 9))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,rows,lda,ldc,sfa_rows", dense_shapes())
+def test_fp8_gemm_random(M, N, K, rows, lda, ldc, sfa_rows):
+    print(f"fp8 gemm {M}x{N}x{K} rows={rows} lda={lda} ldc={ldc} sfa_rows={sfa_rows}", flush=True)
+    a, sfa = quant_act(M, K, rows, lda, sfa_rows, seed=M + 3 * N + K)
+    w, sfb = quant_weight(N, K, seed=N + 5 * K)
+    ref32 = ref.fp8_gemm(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
+    S = ref.fp8_gemm_abs(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
+    Wb = ref.fp8_window_bound(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
+    c = filled((rows, ldc), SENTINEL, torch.int16)
+    ops.fp8_gemm(d(a), d(w), d(sfa), d(sfb), c, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
+    out = h(c, np.uint16)
+    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"random {M}x{N}x{K}", Wb)
+    assert np.all(out[:M, N:] == SENTINEL) and np.all(out[M:] == SENTINEL)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_fp8_gemm_psum_random(seed):
+    rng = np.random.default_rng(seed)
+    groups = int(rng.choice([1, 5, 256]))
+    n, k = int(rng.choice([256, 512, 768])), 128 * int(rng.integers(1, 7))
+    counts = np.where(rng.random(groups) < 0.7, rng.integers(1, 700, groups), 0).astype(np.int32)
+    psum = ref.moe_psum(counts, groups)
+    rows = int((psum[-1] + 127) // 128 * 128) + 128 * int(rng.integers(1, 4))
+    print(f"psum gemm groups={groups} n={n} k={k} rows={rows}", flush=True)
+    a, sfa = quant_act(rows, k, rows, k, rows, seed=seed + 40)
+    w, sfb = quant_weight(n, k, seed=seed + 41, groups=groups)
+    ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows, abs_too=True)
+    Wb = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
+    c = filled((rows, n), SENTINEL, torch.int16)
+    ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows,
+                      groups=groups)
+    out = h(c, np.uint16)
+    owned = ~torch.isnan(ref32[:, 0]).numpy()
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum seed={seed}", Wb[owned])
+    assert np.all(out[~owned] == SENTINEL)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_topk_prefill_random(seed):
+    rng = np.random.default_rng(100 + seed)
+    k = int(rng.choice([1, 7, 64, 333, 2048]))
+    R = int(rng.integers(3, 12))
+    stride0 = 4 * int(rng.integers(k // 4 + 1, 16385))
+    starts = rng.integers(0, 64, R).astype(np.int32)
+    ends = np.minimum(starts + rng.integers(0, stride0, R), stride0).astype(np.int32)
+    print(f"topk seed={seed} k={k} rows={R} stride0={stride0}", flush=True)
+    scale = rng.uniform(1e-3, 1e3, (R, 1))
+    logits = (rng.standard_normal((R, stride0)) * scale).astype(np.float32)
+    if seed % 2 == 0:
+        logits = np.round(logits * 4) / 4                         # ties
+    logits = logits.astype(np.float32)
+    want = ref.topk_prefill(logits, starts, ends, k)
+    out = torch.full((R, k), -7, dtype=torch.int32, device=DEV)
+    ops.topk_prefill(d(logits), d(starts), d(ends), out, R, stride0, topk=k)
+    assert np.array_equal(h(out, np.int32), want)
