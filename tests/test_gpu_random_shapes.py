@@ -85,3 +85,59 @@ def test_topk_prefill_random(seed):
     out = torch.full((R, k), -7, dtype=torch.int32, device=DEV)
     ops.topk_prefill(d(logits), d(starts), d(ends), out, R, stride0, topk=k)
     assert np.array_equal(h(out, np.int32), want)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_quant_and_silu_random(seed):
+    """glm_quant and glm_silu_mul_quant at random row counts, widths, strides and scale-row counts, with
+    magnitudes spread over many binades; bit for bit."""
+    from kern_glm53_amd import synth
+    from tests._gpu import bf16_bits
+    rng = np.random.default_rng(300 + seed)
+    T, K = int(rng.integers(1, 400)), 128 * int(rng.integers(1, 50))
+    ldx, sf_rows = K + 8 * int(rng.integers(0, 5)), T + int(rng.integers(0, 9))
+    print(f"quant T={T} K={K} ldx={ldx} sf_rows={sf_rows}", flush=True)
+    g = synth.generator(400 + seed)
+    xf = torch.randn(T, ldx, generator=g) * torch.exp2(torch.randint(-20, 20, (T, 1), generator=g).float())
+    x = bf16_bits(xf.to(torch.bfloat16))
+    q_ref = np.full((T, K), 0x5a, np.uint8)
+    sf_ref = np.full(ref.sf_words(K) * sf_rows * 4, 0xa5, np.uint8)
+    ref.quant(np.ascontiguousarray(x), K, sf_rows, T, q_ref, sf_ref)
+    q = filled((T, K), 0x5a)
+    sf = filled((ref.sf_words(K) * sf_rows * 4,), 0xa5)
+    ops.quant(d(np.ascontiguousarray(x)), ldx, q, sf, sf_rows, K, T)
+    assert np.array_equal(h(q, np.uint8), q_ref) and np.array_equal(h(sf, np.uint8), sf_ref)
+    rows, I = int(rng.integers(1, 300)), 128 * int(rng.integers(1, 40))
+    n = int(rng.integers(0, rows + 1))
+    sf_rows = rows + int(rng.integers(0, 5))
+    print(f"silu_mul_quant rows={rows} I={I} n={n} sf_rows={sf_rows}", flush=True)
+    gu = bf16_bits((torch.randn(rows, 2 * I, generator=g) * 4).to(torch.bfloat16))
+    q_ref = np.full((rows, I), 0x33, np.uint8)
+    sf_ref = np.full(ref.sf_words(I) * sf_rows * 4, 0x44, np.uint8)
+    ref.silu_mul_quant(gu, I, sf_rows, n, rows, q_ref, sf_ref)
+    q = filled((rows, I), 0x33)
+    sf = filled((ref.sf_words(I) * sf_rows * 4,), 0x44)
+    ops.silu_mul_quant(d(gu), I, q, sf, sf_rows, torch.tensor([n], dtype=torch.int32, device=DEV), rows)
+    assert np.array_equal(h(q, np.uint8), q_ref) and np.array_equal(h(sf, np.uint8), sf_ref)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_bf16_batched_random(seed):
+    """The head-batched bf16 GEMM at random heads, rows, widths and K, with padded row / head strides."""
+    from kern_glm53_amd import synth
+    from tests.test_gpu_gemm import bf16_ref_check
+    rng = np.random.default_rng(500 + seed)
+    heads, m = int(rng.integers(1, 9)), int(rng.integers(1, 700))
+    n, k = 8 * int(rng.integers(1, 70)), 64 * int(rng.integers(1, 12))
+    rows = m + int(rng.integers(0, 5))
+    print(f"bf16 batched heads={heads} m={m} n={n} k={k}", flush=True)
+    g = synth.generator(600 + seed)
+    ka, kd = k + 8 * int(rng.integers(0, 3)), n + 8 * int(rng.integers(0, 3))
+    A = torch.randn(rows, heads, ka, generator=g).to(torch.bfloat16)
+    B = (torch.randn(heads, n, ka, generator=g) * 0.05).to(torch.bfloat16)
+    D = filled((rows, heads, kd), SENTINEL, torch.int16)
+    ops.bf16_batched(A.to(DEV), B.to(DEV), D, m, n=n, k=k, rows=rows, a_strides=(heads * ka * 2, ka * 2),
+                     b_strides=(ka * 2, n * ka * 2), d_strides=(heads * kd * 2, kd * 2), heads=heads)
+    out = h(D, np.uint16)
+    bf16_ref_check(np.ascontiguousarray(out[:m, :, :n]), A[:m, :, :k], B[:, :, :k], k, f"random seed={seed}")
+    assert np.all(out[:m, :, n:] == SENTINEL) and np.all(out[m:] == SENTINEL)
