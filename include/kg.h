@@ -28,8 +28,9 @@ extern "C" {
  * [k/512][n] (one word per weight row); c: bf16 [rows][ldc], columns [n, ldc) untouched.
  * Requires k % 128 == 0, m <= rows <= sfa_rows, n <= ldc, k <= lda, lda % 16 == 0, ldc % 4 == 0, a and w
  * 16-byte aligned, c 8-byte aligned; with 256 or more tiles of 256 x 256 (the persistent kernel, taken
- * when n % 8 == 0, ldc % 8 == 0 and c is 16-byte aligned) also rows * lda, n * k, 256 * lda and
- * rows * ldc * 2 below 2^31 (the byte ranges of its buffer resources). */
+ * when n % 8 == 0, ldc % 8 == 0 and c is 16-byte aligned) also rows * lda and rows * ldc * 2 below 2^31;
+ * always n * k, 256 * lda and the scale arrays' bytes (4 ceil(k/512) sfa_rows, 4 ceil(k/512) n) below
+ * 2^31 (the byte ranges of the kernels' buffer resources and their 32-bit offsets). */
 int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, void* c, int m, int n, int k,
                 int rows, int lda, int ldc, int sfa_rows, void* stream);
 
@@ -39,7 +40,8 @@ int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const void* sfb, 
  * the same rows of A with weight rows [g n, (g+1) n) and scale words [g k/512, (g+1) k/512).  Rows no group
  * owns are left untouched.  psum: device int32 [groups] (glm_moe_psum's output).  Requires n % 8 == 0,
  * ldc % 8 == 0, c 16-byte aligned, a and w 16-byte aligned, rows % 128 == 0, k % 128 == 0, lda % 16 == 0,
- * groups <= 1024, and rows * lda, n * k, 256 * lda, rows * ldc * 2 below 2^31. */
+ * groups <= 1024, and rows * lda, n * k, 256 * lda, rows * ldc * 2 and the scale arrays' bytes per group
+ * (4 ceil(k/512) sfa_rows, 4 ceil(k/512) n) below 2^31. */
 int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, const void* sfb, void* c, const int* psum,
                      int groups, int n, int k, int rows, int lda, int ldc, int sfa_rows, void* stream);
 
@@ -76,7 +78,8 @@ int kg_gemm_bf16_f32(const void* a, const void* b, void* c, int m, int n, int k,
  * r < num_q and j < ke[r] - ks[r],
  *   logits[r * stride + j] = sum_{h<32} w[r][h] * relu(ksf[ks[r]+j] * sum_{d<128} q[r][h][d] kv[ks[r]+j][d]).
  * q: e4m3 [num_q][32][128]; kv: e4m3 [num_kv][128]; ksf f32 [num_kv] (powers of two > 0); w f32 [num_q][32];
- * ks, ke: uint32 [num_q] with ks <= ke <= num_kv; entries at or past ke - ks are unspecified. */
+ * ks, ke: uint32 [num_q] with ks <= ke <= num_kv; entries at or past ke - ks are unspecified.  Requires
+ * 128 num_kv and 4 stride below 2^31. */
 int kg_mqa_logits(const void* q, const void* kv, const float* ksf, const float* w, const unsigned* ks,
                   const unsigned* ke, float* logits, int num_q, int num_kv, int stride, void* stream);
 
@@ -171,7 +174,11 @@ int kg_kv_dequant(const void* kv, const int* block_table, int max_pages, const i
  * three launches as there).  ids int32 [T][topk] -> counts [2*experts] (upper half zero), cta_batch /
  * cta_limit [ctas], num_non_exiting [1], total_padded [1], route_map [mcap], exp2perm [T][topk];
  * expert e's rows start at 2^tile_log2 times its CTA offset and, within an expert, follow ascending
- * expanded index.  Requires experts <= 1024, topk <= 16, T * topk <= 4194304. */
+ * expanded index.  Requires experts <= 256 (the reference's op has 256), topk <= 16, T * topk <= 4194304,
+ * route_map of at least topk*T + experts*2^tile_log2 entries and cta_batch / cta_limit of at least
+ * ceil(topk*T / 2^tile_log2) + experts (the reference's mcap = 8T + 256*128 and mcap/128, gen.py:86-87).
+ * The segment table is a 1 MiB static device array of the library: calls on one device must be
+ * stream-ordered. */
 int kg_moe_routing(const int* ids, int T, int topk, int experts, int tile_log2, int* counts, int* cta_batch,
                    int* cta_limit, int* num_non_exiting, int* total_padded, int* route_map, int* exp2perm,
                    void* stream);
@@ -196,13 +203,16 @@ int kg_moe_combine(const void* fc2, const int* exp2perm, const float* wts, const
 int kg_router_topk(const float* S, const float* bias, const void* rs, int* idx, float* wts, int B, void* stream);
 
 /* glm_requant (source/glm_prep.cu:30-74): e4m3 w [rows][K] with f32 128x128 block scales s
- * [ceil(rows/128)][K/128] re-quantized to UE8M0 blocks into wq / sf (see there for the row mapping).
- * Requires K % 128 == 0 and group_rows % 128 == 0. */
+ * [ceil(rows/128)][K/128] re-quantized to UE8M0 blocks: v = f32(w) s, e = UE8M0(block max |v|, eps 1e-4),
+ * wq = e4m3(v / 2^(e-127)).  Source row r = g group_rows + ri lands in wq row g dst_group_rows + dst_row0 + ri
+ * and its exponent byte in byte kb & 3 of sf word g sf_group + (kb >> 2) sf_ld + dst_row0 + ri.
+ * Requires K % 128 == 0, group_rows % 128 == 0, w and wq 8-byte aligned. */
 int kg_requant(const void* w, const float* s, void* wq, void* sf, int rows, int K, int group_rows,
                int dst_group_rows, int dst_row0, int sf_ld, long long sf_group, void* stream);
 
 /* glm_kvb (source/glm_prep.cu:76-85): kv_b e4m3 [64*448][512] with f32 scales [224][4] -> bf16 kvb
- * [64*448][512] and W_UK transposed per head, wuk [64][512][192]. */
+ * [64*448][512] and W_UK transposed per head, wuk [64][512][192].  Requires w, kvb and wuk 16-byte
+ * aligned. */
 int kg_kvb(const void* w, const float* s, void* kvb, void* wuk, void* stream);
 
 /* Library identification: a static string (build flags, target). */

@@ -129,7 +129,6 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
     compute(st0);
     __syncthreads();
   }
-  kg_mfma_drain();
 
   if constexpr (F32OUT) {
     // f32 out: lane (lane & 31, lane >> 5) holds columns 8 c + 4 (lane >> 5) .. + 3 of row 32 j + (lane & 31)

@@ -77,10 +77,11 @@ KG_DEV u32 kg_ue8m0(float amax, float eps) {
 KG_DEV float kg_exp2i(u32 e) { return kg_u2f(e << 23); }
 
 // The path's exp (see the file comment).  Evaluated with explicit fmaf so contraction cannot change it.
+// Branch-free: the reduction and polynomial run for every x (their value past the range is discarded), and
+// the two range tests select at the end, so a wave never splits on them.
 KG_DEV float kg_exp(float x) {
-  if (x > 88.72283935546875f) return __builtin_inff();
-  if (x < -103.97208404541015625f) return 0.0f;
-  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  const float xr = fminf(fmaxf(x, -104.0f), 89.0f);          // keeps n and ldexp's exponent finite
+  const float n = __builtin_rintf(xr * 1.44269502162933349609375f);
   float r = __builtin_fmaf(n, -0.693145751953125f, x);
   r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
   float p = 1.98412698412698412698e-04f;
@@ -91,7 +92,8 @@ KG_DEV float kg_exp(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  return __builtin_ldexpf(p, (int)n);
+  const float v = __builtin_ldexpf(p, (int)n);            // a NaN x reaches here through r
+  return x > 88.72283935546875f ? __builtin_inff() : (x < -103.97208404541015625f ? 0.0f : v);
 }
 
 // SiLU(g) * u rounded to bf16 and back, as source/glm_glue.cu:192 with the path's exp.
@@ -99,15 +101,13 @@ KG_DEV float kg_silu_mul_bf16(float g, float u) {
   return kg_bf16_to_f32(kg_f32_to_bf16(g / (1.0f + kg_exp(-g)) * u));
 }
 
-// Drains the matrix pipe before an epilogue: no instruction may be scheduled across this point, and
-// 64 wait states cover a full 16-pass v_mfma_scale_f32_32x32x64_f8f6f4.  Without it the compiler may
-// interleave the first epilogue instructions (v_accvgpr_read into VGPRs freed by register allocation)
-// with the last MFMAs still reading those VGPRs as operands; measured on gfx950 as ~3% of fused-epilogue
-// outputs one e4m3 code off, gone with the fence.
-KG_DEV void kg_mfma_drain() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7\n s_nop 7" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
+// This lane's id within the wave (v_mbcnt), formed where it is used: the empty asm makes the value opaque,
+// so address arithmetic built on it is not hoisted out of a loop into registers the loop needs.  The
+// v_mbcnt instructions themselves are the compiler's, so its hazard checks see them.
+KG_DEV int kg_lane_here() {
+  int l = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  asm volatile("" : "+v"(l));
+  return l;
 }
 
 // Max over groups of `width` consecutive lanes (width a power of two <= 64).

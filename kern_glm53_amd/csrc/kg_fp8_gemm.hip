@@ -73,33 +73,41 @@ KG_DEV int kg_wrow(int n0, int half, int r) {
 // rows one ds_read_b128 phase touches then cover all 64 banks once.  A DMA instruction covers 8 rows
 // starting at a multiple of 8, so its lanes' swizzle depends on the instruction's parity only: the lane
 // offsets va / vw (row-in-8 and swizzled chunk) come in an even and an odd version.
+//
+// A buffer load's range check covers its VGPR offset only, not the scalar one: the row offsets go into the
+// VGPR offset and K into the scalar one, and a K block at or past k (the pipeline runs two blocks ahead of
+// the MFMAs) gets the VGPR offset KG_OOB, past every resource, so it reads zeros and touches no memory.
+constexpr unsigned KG_OOB = 0x80000000u;
 template <int NQA, int NQB, int SA>
 KG_DEV void kg_fp8_issue(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
-                         const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko) {
-  // a buffer load's range check covers its VGPR offset only: the row offsets go there, K into the scalar
+                         const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko, int k) {
+  const bool live = ko < k;
 #pragma unroll
   for (int q = 0; q < NQA; ++q)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16,
-                                             va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda), ko, 0, 0);
+                                             live ? va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda) : KG_OOB,
+                                             ko, 0, 0);
 #pragma unroll
   for (int q = 0; q < NQB; ++q)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q) * 1024), 16,
-                                             vw[q & 1] + (unsigned)woff[q], ko, 0, 0);
+                                             live ? vw[q & 1] + (unsigned)woff[q] : KG_OOB, ko, 0, 0);
 }
 
 // DMA instruction q of one K block for this wave: q < NQA an A chunk, else a W chunk.
 template <int NQA, int NQB, int SA>
 KG_DEV void kg_fp8_dma(u8* stage, int wave, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rw,
-                       const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko, int q) {
+                       const unsigned* va, const unsigned* vw, int lda, const int* woff, int ko, int k, int q) {
+  const bool live = ko < k;
   if (q < NQA)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * NQA + q) * 1024), 16,
-                                             va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda), ko, 0, 0);
+                                             live ? va[q & 1] + (unsigned)((wave * NQA + q) * 8 * lda) : KG_OOB,
+                                             ko, 0, 0);
   else
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (KG_LDS void*)(stage + SA + (wave * NQB + q - NQA) * 1024), 16,
-                                             vw[(q - NQA) & 1] + (unsigned)woff[q - NQA], ko, 0, 0);
+                                             live ? vw[(q - NQA) & 1] + (unsigned)woff[q - NQA] : KG_OOB, ko, 0, 0);
 }
 
-// Epilogue of one BM x BN output tile held in acc (after the K loop and kg_mfma_drain): bf16 stores of the
+// Epilogue of one BM x BN output tile held in acc (after the K loop): bf16 stores of the
 // rows [m0, m_end) and columns [n0, n).
 template <int BM, int BN>
 KG_DEV void kg_fp8_epilogue(const KgFp8Args& p, v16f (&acc)[BN / 64][BM / 64], int m0, int m_end, int n0,
@@ -265,7 +273,7 @@ __global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
       }                                                                                                   \
     }                                                                                                     \
     /* second half: K half 1 of CUR; barrier; next step's scale words, its K half 0 from NXT, and the DMA \
-       of K block kt + 2 into CUR (past the last K block these read zeros / unused data, harmlessly) */   \
+       of K block kt + 2 into CUR (past the last K block: VGPR offset KG_OOB, zeros, no memory access) */ \
     _Pragma("unroll") for (int o = 0; o < NO; ++o) {                                                       \
       _Pragma("unroll") for (int n = 0; n < NI; ++n) {                                                     \
         KG_MFMA_ON(o, n, str[o & 1], res[1][n]);                                                          \
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
           _Pragma("unroll") for (int u = 0; u < NIT; ++u) {                                                \
             if (u * NSLOT / NIT != o * NI + n - BAR - 1) continue;                                         \
             if (u < NI) res[0][u] = KG_FRAG_I(NXT, 0, u);                                                   \
-            else kg_fp8_dma<NQA, NQB, SA>(CUR, wave, ra, rw, va, vw, p.lda, woff, (kt_ + 2) * 128, u - NI); \
+            else kg_fp8_dma<NQA, NQB, SA>(CUR, wave, ra, rw, va, vw, p.lda, woff, (kt_ + 2) * 128, p.k, u - NI); \
           }                                                                                               \
         }                                                                                                 \
         __builtin_amdgcn_sched_barrier(0);                                                                \
@@ -288,10 +296,10 @@ __global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
   } while (0)
 
   // prologue: K block 0 in stage 0, K block 1 on its way into stage 1, block 0's first-half fragments read
-  kg_fp8_issue<NQA, NQB, SA>(st0, wave, ra, rw, va, vw, p.lda, woff, 0);
+  kg_fp8_issue<NQA, NQB, SA>(st0, wave, ra, rw, va, vw, p.lda, woff, 0, p.k);
   KG_LOAD_WORDS(0, wa, wb);
   __syncthreads();
-  kg_fp8_issue<NQA, NQB, SA>(st1, wave, ra, rw, va, vw, p.lda, woff, 128);
+  kg_fp8_issue<NQA, NQB, SA>(st1, wave, ra, rw, va, vw, p.lda, woff, 128, p.k);
   str[0] = KG_FRAG_O(st0, 0, 0);
 #pragma unroll
   for (int n = 0; n < NI; ++n) res[0][n] = KG_FRAG_I(st0, 0, n);
@@ -314,7 +322,6 @@ __global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
 #undef KG_MFMA
 
   // ---- epilogue
-  kg_mfma_drain();
   kg_fp8_epilogue<BM, BN>(p, acc, m0, m_end, n0, lane, wn, arow0);
 }
 
@@ -380,7 +387,6 @@ KG_DEV KgPTile kg_ptile(const KgFp8Args& p, const int* tp, const int* ps, int to
 // Where a tile's operands start: A rows from m0 (VGPR offset base), the expert's W panel (resource) and
 // the column tile's first W row (VGPR offset base).  Branch-free: "no tile" (g < 0) is an A base past
 // every resource (KG_OOB) and an empty W resource, so its loads read zeros.
-constexpr unsigned KG_OOB = 0x80000000u;
 struct KgDmaSrc {
   __amdgpu_buffer_rsrc_t rw;
   unsigned abase, wbase;
@@ -408,10 +414,9 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 // row per instruction) skipped the staging but ran q_b at 0.86 ms: whole-line row segments matter most.
 KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, int m0, int m_end,
                                 int n0, int wm, int wn, bool half) {
-  // The lane id comes from a volatile read, so that the per-lane addresses below are computed here, per
-  // tile, rather than hoisted out of the tile loop into registers the K loop needs.
-  int lane;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  // the lane id formed here, so that the per-lane addresses below are computed per tile rather than hoisted
+  // out of the tile loop into registers the K loop needs
+  const int lane = kg_lane_here();
   const __amdgpu_buffer_rsrc_t rc = kg_rsrc(p.c, (long long)p.rows * p.ldc * 2);
   const int mr = lane & 31;                       // this lane's row of the MFMA tile
   u8* const wrow = stage + mr * 128 + ((lane >> 5) << 3);
@@ -460,8 +465,7 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
 // stores and 1 exponent-byte store (offsets past the resource drop the rows past the tile).
 KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, float (*xam)[256], u8* xe,
                                  int wave, int m0, int m_end, int nt, int wm, int wn, bool half) {
-  int lane;   // from a volatile read: keeps the per-lane address math here rather than hoisted
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  const int lane = kg_lane_here();   // keeps the per-lane address math here rather than hoisted
   const int hn = p.n >> 1;
   const int arow0 = (half ? wm * 64 : wm * 128) + (lane & 31);   // a half tile's waves own 64 rows each
 #pragma unroll
@@ -660,10 +664,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // stages before it is needed.
   u32 wa[2][TJ], wb[2][TI];
   auto words = [&](const KgPTile& t, int kg4, u32* xa, u32* xb) {
-    // the lane id from a volatile read: the per-lane word offsets are formed here rather than kept in
+    // the lane id formed here: the per-lane word offsets are formed at the loads rather than kept in
     // registers across the K loop (spilled, their reloads would wait for the whole DMA queue)
-    int ln;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int ln = kg_lane_here();
     const __amdgpu_buffer_rsrc_t rsb =
         kg_rsrc(p.sfb + (size_t)(t.g > 0 ? t.g : 0) * kw * p.n, t.g >= 0 ? (long long)kw * p.n * 4 : 0);
     const int arow0 = wm * (BM / 2) + (ln & 31);
@@ -892,7 +895,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     }
 #undef KG_GROUP_START
 #undef KG_GROUP_END
-    kg_mfma_drain();
     if constexpr (MODE == 2) {
       // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
       kg_fp8_epilogue_silu(p, acc, st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
@@ -964,6 +966,9 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
   KG_CHECK(m >= 0 && n > 0 && k > 0 && k % 128 == 0 && m <= rows && rows <= sfa_rows && n <= ldc && k <= lda);
   KG_CHECK(lda % 16 == 0 && ldc % 4 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(c, 8));
   KG_CHECK(kg_aligned(sfa, 4) && kg_aligned(sfb, 4));
+  // byte ranges of the buffer resources and 32-bit offsets of both kernels
+  KG_CHECK((long long)n * k < (1ll << 31) && 256ll * lda < (1ll << 31));
+  KG_CHECK((long long)((k + 511) >> 9) * sfa_rows * 4 < (1ll << 31) && (long long)((k + 511) >> 9) * n * 4 < (1ll << 31));
   if (m == 0) return 0;
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
@@ -990,6 +995,7 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
   KG_CHECK(lda % 16 == 0 && ldc % 8 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(c, 16));
   KG_CHECK((long long)rows * ldc * 2 < (1ll << 31));
   KG_CHECK(kg_aligned(sfa, 4) && kg_aligned(sfb, 4));
+  KG_CHECK((long long)((k + 511) >> 9) * sfa_rows * 4 < (1ll << 31) && (long long)((k + 511) >> 9) * n * 4 < (1ll << 31));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
   p.psum = psum, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows;
@@ -1010,6 +1016,8 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   KG_CHECK(lda % 16 == 0 && kg_aligned(a, 16) && kg_aligned(w, 16) && kg_aligned(q, 16));
   KG_CHECK((long long)rows * (n / 2) < (1ll << 31));
   KG_CHECK(kg_aligned(sfa, 4) && kg_aligned(sfb, 4));
+  KG_CHECK((long long)((k + 511) >> 9) * sfa_rows * 4 < (1ll << 31) && (long long)((k + 511) >> 9) * n * 4 < (1ll << 31));
+  KG_CHECK((long long)((n / 2 + 511) >> 9) * sf_rows * 4 < (1ll << 31));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb;
   p.psum = psum, p.q = (u8*)q, p.qsf = (u8*)sf, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda;

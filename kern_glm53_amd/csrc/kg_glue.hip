@@ -108,7 +108,7 @@ extern "C" int kg_silu_mul_quant(const void* gu, int I, void* q, void* sf, int s
 //      round plus the segment's running per-expert counters give the base.
 #define KG_SEG 4096
 #define KG_MAX_SEGS 1024
-#define KG_MAX_EXPERTS 1024
+#define KG_MAX_EXPERTS 256     // the reference's routing op is routing(EXPERTS = 256, ...) (scripts/gen.py:146)
 
 // Scratch shared by all routing calls on a device: calls on one device must be stream-ordered.
 static __device__ __align__(256) int kg_route_seg[KG_MAX_SEGS * KG_MAX_EXPERTS];
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void kg_route_count(const int* __restrict__ id
   for (int e = threadIdx.x; e < experts; e += 256) kg_route_seg[(size_t)s * experts + e] = hist[e];
 }
 
-__global__ __launch_bounds__(1024) void kg_route_plan(int nseg, int experts, int tile_log2, int* __restrict__ counts,
+__global__ __launch_bounds__(KG_MAX_EXPERTS) void kg_route_plan(int nseg, int experts, int tile_log2, int* __restrict__ counts,
                                                       int* __restrict__ cta_batch, int* __restrict__ cta_limit,
                                                       int* __restrict__ nne, int* __restrict__ tpad) {
   __shared__ int scan[KG_MAX_EXPERTS];
@@ -216,6 +216,9 @@ extern "C" int kg_moe_routing(const int* ids, int T, int topk, int experts, int 
                               int* cta_batch, int* cta_limit, int* num_non_exiting, int* total_padded,
                               int* route_map, int* exp2perm, void* stream) {
   KG_CHECK(ids && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm);
+  // experts <= 256 keeps the padded rows (at most topk * T + experts * (2^tile_log2 - 1)) and the row blocks
+  // within the reference's buffers, route_map [topk * T + 256 * 128] and cta_* [that / 128]
+  // (scripts/gen.py:86-87, 289-293), at its tile of 128
   KG_CHECK(T >= 0 && topk >= 1 && topk <= 16 && experts >= 1 && experts <= KG_MAX_EXPERTS && tile_log2 >= 0 &&
            tile_log2 <= 10);
   const long long total = (long long)T * topk;
@@ -224,7 +227,7 @@ extern "C" int kg_moe_routing(const int* ids, int T, int topk, int experts, int 
   hipStream_t st = (hipStream_t)stream;
   if (nseg > 0)
     hipLaunchKernelGGL(kg_route_count, dim3(nseg), dim3(256), 0, st, ids, (int)total, experts);
-  hipLaunchKernelGGL(kg_route_plan, dim3(1), dim3(1024), 0, st, nseg, experts, tile_log2, counts, cta_batch,
+  hipLaunchKernelGGL(kg_route_plan, dim3(1), dim3(KG_MAX_EXPERTS), 0, st, nseg, experts, tile_log2, counts, cta_batch,
                      cta_limit, num_non_exiting, total_padded);
   if (nseg > 0)
     hipLaunchKernelGGL(kg_route_rank, dim3(nseg), dim3(256), 0, st, ids, (int)total, experts, topk, route_map,

@@ -188,7 +188,8 @@ extern "C" int kg_mqa_logits(const void* q, const void* kv, const float* ksf, co
                              const unsigned* ke, float* logits, int num_q, int num_kv, int stride, void* stream) {
   KG_CHECK(q && kv && ksf && w && ks && ke && logits && num_q >= 0 && num_kv >= 0 && stride >= 0);
   KG_CHECK(kg_aligned(q, 16) && kg_aligned(kv, 16) && kg_aligned(ksf, 4) && kg_aligned(logits, 4));
-  KG_CHECK((long long)num_kv * 128 < (1ll << 31));
+  // the byte ranges of the key resource and of one logits row (its store offsets are 32-bit)
+  KG_CHECK((long long)num_kv * 128 < (1ll << 31) && (long long)stride * 4 < (1ll << 31));
   if (num_q == 0) return 0;
   hipLaunchKernelGGL(kg_mqa_logits_kernel, dim3((num_q + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                      (const u8*)q, (const u8*)kv, ksf, w, ks, ke, logits, num_q, num_kv, stride);

@@ -69,6 +69,10 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     ("kg_fp8_gemm", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 256, 128, 16, 128, 128, 16, NULL]),
     # rows > sfa_rows
     ("kg_fp8_gemm", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 128, 128, 32, 128, 128, 16, NULL]),
+    # 32-bit byte offsets: n * k >= 2^31 (tile kernel too), 256 * lda >= 2^31, scale words past 2^31 bytes
+    ("kg_fp8_gemm", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 131072, 16384, 16, 16384, 131072, 16, NULL]),
+    ("kg_fp8_gemm", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 128, 128, 16, 1 << 23, 128, 16, NULL]),
+    ("kg_fp8_gemm", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 128, 65536, 16, 65536, 128, 1 << 22, NULL]),
     # grouped: rows not a multiple of 128, too many groups
     ("kg_fp8_gemm_psum", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 256, 100, 256, 256, 100, NULL]),
     ("kg_fp8_gemm_psum", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2048, 256, 256, 128, 256, 256, 128, NULL]),
@@ -83,8 +87,9 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     ("kg_quant", [FAKE, 6144, FAKE, FAKE, 16, 6144, 17, NULL]),
     ("kg_quant", [FAKE, 6145, FAKE, FAKE, 16, 6144, 16, NULL]),
     ("kg_silu_mul_quant", [FAKE, 100, FAKE, FAKE, 16, NULL, 16, NULL]),
-    # routing: too many experts / topk
+    # routing: too many experts (the reference's buffers hold 256 experts' padding) / topk
     ("kg_moe_routing", [FAKE, 16, 8, 2048, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
+    ("kg_moe_routing", [FAKE, 16, 8, 257, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
     ("kg_moe_routing", [FAKE, 16, 32, 256, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
     # gather: T > x_rows
     ("kg_moe_gather", [FAKE, FAKE, 8, FAKE, FAKE, FAKE, 1024, 16, NULL]),
@@ -94,8 +99,9 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     # library GEMMs: k % 64, ldc < n
     ("kg_gemm_bf16", [FAKE, FAKE, FAKE, 16, 32, 100, 32, NULL]),
     ("kg_gemm_bf16_f32", [FAKE, FAKE, FAKE, 16, 256, 6144, 128, NULL]),
-    # mqa: negative sizes
+    # mqa: negative sizes, a row stride whose byte offsets pass 2^31
     ("kg_mqa_logits", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, 16, 256, NULL]),
+    ("kg_mqa_logits", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 16, 1 << 29, NULL]),
     # add_rms_quant: T > sf_rows, q without sf
     ("kg_add_rms_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 17, NULL]),
     ("kg_add_rms_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 16, 16, NULL]),

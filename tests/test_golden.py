@@ -63,8 +63,8 @@ def test_oracle_gemm():
     assert np.array_equal(w, f["w"]) and np.array_equal(sfb, f["sfb"])
     c = ref.fp8_gemm(f["a"], f["w"], f["sfa"], f["sfb"], M, N, K, K, M)
     out = torch.from_numpy(f["c_bf16"].view(np.int16)).view(torch.bfloat16).float()
-    ok, rel, ratio = ref.check_bf16_gemm(out, c, torch.from_numpy(f["abs_sum"]), K)
-    assert ok and rel < 1e-4
+    ok, rep = ref.check_bf16_gemm(out, c, torch.from_numpy(f["abs_sum"]), K)
+    assert ok and rep["rel_l2"] < 1e-4
 
 
 def test_oracle_mqa():
@@ -142,9 +142,10 @@ def test_gpu_golden_gemm_and_logits():
     ops.fp8_gemm(d(f["a"]), w, d(f["sfa"]), sfb, c, M, n=N, k=K, rows=M, lda=K, ldc=N, sfa_rows=M)
     out = torch.from_numpy(h(c, np.int16)).view(torch.bfloat16).float()
     ref32 = torch.from_numpy(f["c_bf16"].view(np.int16)).view(torch.bfloat16).float()
-    Wb = ref.fp8_window_bound(f["a"], f["w"], f["sfa"], f["sfb"], M, N, K, K, M)
-    ok, rel, ratio = ref.check_bf16_gemm(out, ref32, torch.from_numpy(f["abs_sum"]), K, window=Wb)
-    assert ok, (rel, ratio)
+    model = ref.fp8_gemm_mfma(f["a"], f["w"], f["sfa"], f["sfb"], M, N, K, K, M)
+    ok, rep = ref.check_bf16_gemm(out, ref32, torch.from_numpy(f["abs_sum"]), K, model32=model)
+    print(ref.parity_line("golden fp8 gemm 128x256x512", rep), flush=True)
+    assert ok, ref.parity_line("golden fp8 gemm 128x256x512", rep)
 
     f = load("mqa_logits_8x256")
     nq, nkv, stride = f["q8"].shape[0], f["k8"].shape[0], int(f["stride"])

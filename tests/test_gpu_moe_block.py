@@ -1,8 +1,10 @@
 """The MoE block (kern_glm53_amd.moe, scripts/gen.py:435-448) end to end on the GPU against a reference chain:
 the router GEMM against torch fp32, the router top-k, routing tables, psum and gather against the oracle bit for
-bit, and the block's output h against the oracle's step-by-step restatement (fp32 dequantize-then-matmul GEMMs,
-the oracle's SiLU-mul-quant and fma-chain combine) within the GEMMs' accumulation-order tolerance.  The router's
-bias steers every token to 16 experts (ragged counts among them), which keeps the reference's GEMMs small."""
+bit, and the block's output h against the oracle's step-by-step restatement, twice: with fp32
+dequantize-then-matmul GEMMs (the reference's math, every token, within the GEMMs' accumulation-order
+tolerance) and, for sampled tokens, with the oracle's model of the fp8 MFMA for the four GEMMs, where every bf16
+of h must be equal.  The router's bias steers every token to 16 experts (ragged counts among them), which keeps
+the reference's GEMMs small."""
 import numpy as np
 import pytest
 import torch
@@ -104,3 +106,32 @@ def test_moe_block_against_oracle_chain():
           f" max {r.max():.2e}; rows with ids per expert {np.bincount(ids_ref.ravel(), minlength=LIVE)[:LIVE]}", flush=True)
     assert rel < 1e-2
     assert np.quantile(r, 0.999) < 2.0 ** -6 and r.max() < 2.0 ** -3
+
+    # sampled tokens through the chain with the MFMA model for every fp8 GEMM: h bit for bit
+    xq_h, xsf_w = h(xq, np.uint8), h(xsf, np.uint8).reshape(-1, x_rows, 4)
+    w13_h, sf13_h, w2_h, sf2_h = h(w13, np.uint8), h(sf13, np.uint8), h(w2, np.uint8), h(sf2, np.uint8)
+    kw_h, kw_i = ops.sf_words(H), ops.sf_words(INTER)
+
+    def expert_row(t, wgu, sfgu, wdn, sfdn, e):
+        """One token's row through gate_up (model) -> bf16 -> SiLU-mul-quant -> down (model) -> bf16."""
+        a_t = np.ascontiguousarray(xq_h[t:t + 1])
+        sa_t = np.ascontiguousarray(xsf_w[:, t:t + 1, :])
+        gu = ref.fp8_gemm_mfma(a_t, wgu[e * 2 * INTER:(e + 1) * 2 * INTER], sa_t,
+                               sfgu[e * kw_h * 2 * INTER * 4:(e + 1) * kw_h * 2 * INTER * 4], 1, 2 * INTER, H, H, 1)
+        q, sfq = ref.silu_mul_quant(ref.bf16_round(gu), INTER, 1, None, 1)
+        y = ref.fp8_gemm_mfma(q, wdn[e * H:(e + 1) * H], sfq, sfdn[e * kw_i * H * 4:(e + 1) * kw_i * H * 4], 1, H,
+                              INTER, INTER, 1)
+        return ref.bf16_round(y)[0]
+
+    w_sgu_h, sf_sgu_h, w_sdn_h, sf_sdn_h = h(w_sgu, np.uint8), h(sf_sgu, np.uint8), h(w_sdn, np.uint8), h(sf_sdn, np.uint8)
+    got_bits = h(out.view(torch.int16), np.uint16)
+    sample = sorted({0, T - 1} | set(np.random.default_rng(9).choice(T, 6, replace=False).tolist()))
+    equal = 0
+    for t in sample:
+        f2_t = np.stack([expert_row(t, w13_h, sf13_h, w2_h, sf2_h, int(e)) for e in ids_ref[t]])
+        sh_t = expert_row(t, w_sgu_h, sf_sgu_h, w_sdn_h, sf_sdn_h, 0)[None]
+        h_t = ref.moe_combine(f2_t, np.arange(8, dtype=np.int32).reshape(1, 8), wts_ref[t:t + 1], sh_t, 1)[0]
+        equal += int(np.sum(h_t == got_bits[t]))
+        assert np.array_equal(h_t, got_bits[t]), f"token {t}: {np.sum(h_t != got_bits[t])} of {H} differ"
+    print(f"PARITY moe block with the MFMA model: {len(sample)} tokens, {equal} of {len(sample) * H} bf16 equal",
+          flush=True)

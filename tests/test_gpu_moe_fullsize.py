@@ -2,7 +2,7 @@
 popularity: 131072 routed rows in 163840 row slots): the fused gate_up + SiLU-mul-quant equals the unfused
 chain (the bf16 grouped GEMM, then glm_silu_mul_quant) bit for bit on every owned row, and sampled rows of
 both grouped GEMMs (the largest expert, half-tile and full-tile tails) match the oracle's dequantize-then-
-matmul, every column."""
+matmul (rel-L2) and the oracle's model of the fp8 MFMA, every column."""
 import numpy as np
 import pytest
 import torch
@@ -27,7 +27,7 @@ def scale_bytes(g, n):
 
 
 def oracle_rows(a, sfa, rows_all, w, sfb, e, n, k, sample):
-    """f32 reference, abs-sum and window bound of `sample` rows (all owned by expert e)."""
+    """f32 reference, abs-sum and MFMA-model sum of `sample` rows (all owned by expert e)."""
     kw = ref.sf_words(k)
     a_s = h(a[sample], np.uint8)
     sfa_s = np.ascontiguousarray(h(sfa, np.uint8).reshape(-1, rows_all, 4)[:, sample, :]).reshape(-1)
@@ -35,7 +35,7 @@ def oracle_rows(a, sfa, rows_all, w, sfb, e, n, k, sample):
     sfb_e = h(sfb[e * kw * n * 4:(e + 1) * kw * n * 4], np.uint8)
     R = len(sample)
     return (ref.fp8_gemm(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R), ref.fp8_gemm_abs(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R),
-            ref.fp8_window_bound(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R))
+            ref.fp8_gemm_mfma(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R))
 
 
 def test_moe_gemms_full_size():

@@ -2,7 +2,8 @@
 GEMMs on both kernels (the 128 x 128 tile kernel for small or odd-width outputs, the persistent one for at
 least 256 tiles of 256 x 256) with random tails, strides and scale-row counts; grouped GEMMs with random
 expert counts; top-k rows of random lengths, starts and K.  Each case against the oracle, at the same bars
-as the fixed cases (GEMMs within the f32-accumulation and MFMA-window bounds, top-k bit for bit)."""
+as the fixed cases (fp8 GEMMs: rel-L2 against the fp32 reference and equality with the oracle's model of
+the fp8 MFMA on sampled rows; top-k bit for bit)."""
 import numpy as np
 import pytest
 import torch
@@ -10,7 +11,7 @@ import torch
 from kern_glm53_amd import ops
 from oracle import ref
 from tests._gpu import DEV, d, filled, h
-from tests.test_gpu_gemm import SENTINEL, check, quant_act, quant_weight
+from tests.test_gpu_gemm import SENTINEL, check, model_on_rows, quant_act, quant_weight, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -37,11 +38,11 @@ def test_fp8_gemm_random(M, N, K, rows, lda, ldc, sfa_rows):
     w, sfb = quant_weight(N, K, seed=N + 5 * K)
     ref32 = ref.fp8_gemm(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
     S = ref.fp8_gemm_abs(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
-    Wb = ref.fp8_window_bound(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
+    model = model_on_rows(a, w, sfa, sfb, M, N, K, lda, sfa_rows, sample_rows(M, seed=M))
     c = filled((rows, ldc), SENTINEL, torch.int16)
     ops.fp8_gemm(d(a), d(w), d(sfa), d(sfb), c, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
     out = h(c, np.uint16)
-    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"random {M}x{N}x{K}", Wb)
+    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"random {M}x{N}x{K}", model)
     assert np.all(out[:M, N:] == SENTINEL) and np.all(out[M:] == SENTINEL)
 
 
@@ -57,13 +58,13 @@ def test_fp8_gemm_psum_random(seed):
     a, sfa = quant_act(rows, k, rows, k, rows, seed=seed + 40)
     w, sfb = quant_weight(n, k, seed=seed + 41, groups=groups)
     ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows, abs_too=True)
-    Wb = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
+    model = ref.fp8_gemm_psum_mfma(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
     c = filled((rows, n), SENTINEL, torch.int16)
     ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows,
                       groups=groups)
     out = h(c, np.uint16)
     owned = ~torch.isnan(ref32[:, 0]).numpy()
-    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum seed={seed}", Wb[owned])
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum seed={seed}", model[owned])
     assert np.all(out[~owned] == SENTINEL)
 
 

@@ -143,6 +143,30 @@ def test_quant_properties_and_layout():
     assert np.all(words[:, T:] == 0)
 
 
+def test_head_quant_closed_form():
+    """kgo_head_quant (the indexer's per-(row, head) quant, source/glm_glue.cu:338-342): the scale is
+    2^(e-127) with e the frexp closed form of the head's amax at eps 1e-4, and every code is torch's e4m3
+    cast of x / scale.  Inputs are general f32 values (not bf16), as the rotated indexer query is, over
+    40 binades, with an all-zero head (eps decides) and a head whose amax is an exact power of two x 448."""
+    rng = np.random.default_rng(61)
+    rows, heads = 23, 32
+    x = (rng.standard_normal((rows, heads, 128)) * np.exp2(rng.integers(-20, 20, (rows, heads, 1)))).astype(np.float32)
+    x[2, 5] = 0.0
+    x[4, 7] = 1.0
+    x[4, 7, 3] = -448.0 * 2.0 ** -5
+    q, sc = ref.head_quant(x)
+    for r in range(rows):
+        for hh in range(heads):
+            e = ue8m0_closed_form(np.abs(x[r, hh]).max(), 1e-4)
+            assert sc[r, hh] == np.float32(2.0 ** (e - 127))
+            scaled = (x[r, hh] / np.float32(2.0 ** (e - 127))).astype(np.float32)
+            assert np.all(np.abs(scaled) <= 448)
+            want = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            assert np.array_equal(q[r, hh], want), (r, hh)
+    assert sc[2, 5] == np.float32(2.0 ** (ue8m0_closed_form(0.0, 1e-4) - 127))
+    assert q[4, 7, 3] == 0xfe                   # -448 exactly: the largest code, sign set
+
+
 def test_quant_strided_input():
     rng = np.random.default_rng(6)
     x = ref.bf16_round(rng.standard_normal((9, 700)).astype(np.float32))
