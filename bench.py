@@ -22,6 +22,7 @@ import statistics
 import sys
 import time
 
+import numpy as np
 import torch
 
 METRIC = "FP8 GEMM TFLOP/s + % MFMA peak: dense and 256-expert MoE at M=16384, 1 GPU"
@@ -292,6 +293,10 @@ def aux_prepare(data, dev):
     aux["wuk"] = bf(64, 512, 192)
     aux["qmla"] = torch.zeros(M, 64, 576, dtype=torch.bfloat16, device=dev)
     # W_UV: A = o [r][64][512], B = kvb rows h*448 + 192 + d (row 1024 B, head 458752 B), D = ov [r][64][256]
+    # W_UK in its contiguous K = 128 form: A [r][64][128], B [64][512][128], D [r][64][512]
+    aux["a128"] = bf(M, 64, 128)
+    aux["wuk128"] = bf(64, 512, 128)
+    aux["d128"] = torch.empty(M, 64, 512, dtype=torch.bfloat16, device=dev)
     aux["o"] = bf(M, 64, 512)
     aux["kvb"] = bf(64 * 448, 512)
     aux["ov"] = torch.empty(M, 64, 256, dtype=torch.bfloat16, device=dev)
@@ -327,6 +332,10 @@ def aux_launches(aux):
                                                         a_strides=(40960, 512), b_strides=(384, 196608),
                                                         d_strides=(73728, 1152)),
          2.0 * M * 64 * 512 * 192, M * 64 * (192 + 512) * 2 + 64 * 512 * 192 * 2, "hbm"),
+        ("w_uk_k128_bf16_batched", lambda: ops.bf16_batched(aux["a128"], aux["wuk128"], aux["d128"], M, n=512, k=128,
+                                                             rows=M, a_strides=(64 * 256, 256),
+                                                             b_strides=(256, 512 * 256), d_strides=(64 * 1024, 1024)),
+         2.0 * M * 64 * 512 * 128, M * 64 * (128 + 512) * 2 + 64 * 512 * 128 * 2, "hbm"),
         ("w_uv_bf16_batched", lambda: ops.bf16_batched(aux["o"], aux["kvb"][192:], aux["ov"], M, n=256, k=512, rows=M,
                                                         a_strides=(65536, 1024), b_strides=(1024, 458752),
                                                         d_strides=(32768, 512)),
@@ -345,41 +354,108 @@ def aux_launches(aux):
     ]
 
 
-def time_launch(fn, stream, iters=5):
+def skinny_launches(data, dev):
+    """The MoE GEMMs on psum plans of uniformly skinny experts: each of the 256 experts owns r rows, r = 100 (one
+    128-row block: a half tile) or r = 228 (two blocks: one 256-row tile).  Every launch streams all the experts'
+    weights (6.4 GB gate_up, 3.2 GB down) for little work per byte: the regime of a real routing's
+    low-occupancy experts.  (name, launch, algorithmic flops, algorithmic HBM bytes, expert tiles)."""
+    from kern_glm53_amd import ops
+
+    m = data["moe"]
+    mcap = m["mcap"]
+    out = []
+    for r in (100, 228):
+        blk = (r + 127) // 128
+        psum = torch.tensor([128 * blk * g + r for g in range(EXPERTS)], dtype=torch.int32, device=dev)
+        m[f"psum_{r}"] = psum
+        R = EXPERTS * r
+        out.append((f"gate_up_silu_quant_r{r}",
+                    lambda psum=psum: ops.fp8_gemm_psum_silu_quant(m["mq"], m["w13"], m["msf"], m["sf13"], psum,
+                                                                   m["mq2"], m["msf2"], n=2 * INTER, k=H, rows=mcap,
+                                                                   lda=H, sfa_rows=mcap, sf_rows=mcap),
+                    2.0 * R * 2 * INTER * H,
+                    EXPERTS * 2 * INTER * H + R * H + R * INTER + EXPERTS * 2 * INTER * H // 16384, EXPERTS * 16))
+        out.append((f"down_r{r}",
+                    lambda psum=psum: ops.fp8_gemm_psum(m["mq2"], m["w2"], m["msf2"], m["sf2"], m["f2"], psum, n=H,
+                                                        k=INTER, rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap),
+                    2.0 * R * H * INTER, EXPERTS * H * INTER + R * INTER + R * H * 2 + EXPERTS * H * INTER // 16384,
+                    EXPERTS * 24))
+    return out
+
+
+def time_launch(fn, stream, iters=7):
+    """Median over `iters` launches of one launch's time (HIP events on the launch stream), ms."""
     fn()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(iters):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for e0, e1 in ev:
+        e0.record(stream)
         fn()
-    e1.record(stream)
+        e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
 
 
-def cpu_baseline(data, rows=8192, runs=5):
-    """The oracle's fp32 dequantize-then-matmul (PyTorch-CPU) on rows [0, rows) of each dense GEMM: a bounded
-    sample of about 10 s of CPU work (half of the M = 16384 chunk, five runs)."""
+def cpu_baseline(data, aux, rows=8192, runs=5):
+    """The oracle's reference math on PyTorch-CPU, three bounded legs (about 15 s in all):
+      * dense: fp32 dequantize-then-matmul on rows [0, rows) of each dense GEMM (half the chunk), median of
+        `runs` runs: the headline `value`;
+      * moe: the m-grouped gate_up and down GEMMs per expert (dequantize-then-matmul of each expert's rows
+        against its weights) over the leading experts of the bench's routing that hold at least 4096 rows;
+      * mqa: the f64 MQA logits of the chunk's last 32 query rows (each against its 65505+ causal keys),
+        a row at a time as the oracle evaluates it."""
     from oracle import ref
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
     torch.set_num_threads(threads)
+
+    def timed(fn, n):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
     host = []
     for name, n, k, _ in DENSE:
         t = data[name]
         host.append((t["a"][:rows].cpu().numpy(), t["w"].cpu().numpy(), t["sfa"].cpu().numpy(),
                      t["sfb"].cpu().numpy(), n, k))
     flops = sum(2.0 * rows * n * k for *_, n, k in host)
-    times = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        for a, w, sfa, sfb, n, k in host:
-            ref.fp8_gemm(a, w, sfa, sfb, rows, n, k, k, M)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"rows 0-{rows - 1} of the three dense GEMMs (q_a/kv_a, q_b, o_proj), fp32 dequantize-"
-                      f"then-matmul incl. dequant, median of {runs} runs of {med:.2f} s"}
+    med = timed(lambda: [ref.fp8_gemm(a, w, sfa, sfb, rows, n, k, k, M) for a, w, sfa, sfb, n, k in host], runs)
+    legs = {"dense": {"value": round(flops / med / 1e12, 4), "unit": "TFLOP/s", "seconds": round(med, 3)}}
+
+    m = data["moe"]
+    psum = m["psum"].cpu().numpy()
+    G = int(np.searchsorted(psum, 4096)) + 1              # leading experts holding >= 4096 rows
+    end = int(psum[G - 1])
+    kw1, kw2 = ref.sf_words(H), ref.sf_words(INTER)
+    hm = dict(a1=m["mq"][:end].cpu().numpy(), s1=m["msf"].cpu().numpy(), w1=m["w13"][:G * 2 * INTER].cpu().numpy(),
+              b1=m["sf13"][:G * kw1 * 2 * INTER * 4].cpu().numpy(), a2=m["mq2"][:end].cpu().numpy(),
+              s2=m["msf2"].cpu().numpy(), w2=m["w2"][:G * H].cpu().numpy(), b2=m["sf2"][:G * kw2 * H * 4].cpu().numpy())
+    R = int(sum(max(0, e - s0) for s0, e in ref.psum_ranges(psum[:G])))
+    mflops = 2.0 * R * (2 * INTER * H + H * INTER)
+    mcap = m["mcap"]
+    med = timed(lambda: (ref.fp8_gemm_psum(hm["a1"], hm["w1"], hm["s1"], hm["b1"], psum[:G], G, 2 * INTER, H, end, H,
+                                           mcap),
+                         ref.fp8_gemm_psum(hm["a2"], hm["w2"], hm["s2"], hm["b2"], psum[:G], G, H, INTER, end, INTER,
+                                           mcap)), 3)
+    legs["moe"] = {"value": round(mflops / med / 1e12, 4), "unit": "TFLOP/s", "seconds": round(med, 3),
+                   "sample": f"experts 0-{G - 1} ({R} routed rows), gate_up + down"}
+
+    nq = 32
+    q8, k8 = aux["iq"][-nq:].cpu().numpy(), aux["kg"].cpu().numpy()
+    ksf, w = aux["ksf"].cpu().numpy(), aux["w"][-nq:].cpu().numpy()
+    ks, ke = aux["ks"][-nq:].cpu().numpy(), aux["ke"][-nq:].cpu().numpy()
+    qflops = 2.0 * 32 * 128 * float((ke - ks).sum())
+    med = timed(lambda: ref.mqa_logits(q8, k8, ksf, w, ks, ke, nq, aux["ctx"]), 1)
+    legs["mqa"] = {"value": round(qflops / med / 1e12, 4), "unit": "TFLOP/s", "seconds": round(med, 3),
+                   "sample": f"the last {nq} query rows, f64"}
+    return {"value": legs["dense"]["value"], "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"dense: rows 0-{rows - 1} of the three dense GEMMs (q_a/kv_a, q_b, o_proj), fp32 dequantize-"
+                      f"then-matmul incl. dequant, median of {runs} runs of {legs['dense']['seconds']:.2f} s; "
+                      f"legs: {legs['moe']['sample']} and MQA {legs['mqa']['sample']}",
+            "legs": legs}
 
 
 def main():
@@ -434,7 +510,7 @@ def main():
     ms_step = wall * 1e3 / args.steps
     per = {}
     for i, (name, flops, _) in enumerate(L):
-        ms = statistics.mean(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps))
+        ms = statistics.median(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps))
         per[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
                      "frac_peak": round(flops / (ms * 1e-3) / PEAK_FP8, 4), "gflop": round(flops / 1e9, 2)}
     total_flops = sum(f for _, f, _ in L)
@@ -473,13 +549,21 @@ def main():
                      "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": bound,
                      "frac": round(flops / (ms * 1e-3) / PEAK_FP8 if bound == "mfma" else
                                    nbytes / (ms * 1e-3) / PEAK_HBM, 4)}
-    del aux_data
     log("aux: " + ", ".join(f"{k} {v['ms']:.3f} ms ({v['tflops']:.0f} TF/s, {v['gbps']:.0f} GB/s)" for k, v in aux.items()))
+    skinny = {}
+    for name, fn, flops, nbytes, tiles in skinny_launches(data, dev):
+        ms = time_launch(fn, stream)
+        skinny[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                        "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / PEAK_HBM, 4),
+                        "tiles": tiles, "us_per_tile_per_cu": round(ms * 1e3 * 256 / tiles, 2)}
+    log("skinny experts: " + ", ".join(f"{k} {v['ms']:.3f} ms ({v['tflops']:.0f} TF/s, {v['gbps']:.0f} GB/s)"
+                                       for k, v in skinny.items()))
 
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle, PyTorch-CPU)")
-        cpu = cpu_baseline(data)
+        cpu = cpu_baseline(data, aux_data)
+    del aux_data
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -497,6 +581,7 @@ def main():
         "producers": producers,
         "moe_block": block,
         "aux": aux,
+        "moe_skinny": skinny,
     }
     print(json.dumps(line), flush=True)
 

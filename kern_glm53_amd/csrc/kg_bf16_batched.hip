@@ -70,16 +70,23 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
       kg_rsrc_b(p.a + (size_t)h * p.a_hs + (size_t)m0 * p.a_rs, (long long)(mv - 1) * p.a_rs + 2ll * p.k);
   const __amdgpu_buffer_rsrc_t rb =
       kg_rsrc_b(p.b + (size_t)h * p.b_hs + (size_t)n0 * p.b_rs, (long long)(nv - 1) * p.b_rs + 2ll * p.k);
-  const int chunk = ((lane & 7) ^ (lane >> 3)) << 4;
-  const unsigned va = (unsigned)((lane >> 3) * p.a_rs + chunk);
-  const unsigned vb = (unsigned)((lane >> 3) * p.b_rs + chunk);
+  // LDS row r keeps 16-byte chunk c in slot c ^ ((r >> 1) & 7): the 16 rows of a ds_read_b128 phase then
+  // cover gfx950's 64 banks once.  A DMA instruction fills 8 rows from a multiple of 8, lane l slot l & 7 of
+  // row l >> 3, so its source chunk depends on the instruction's parity only.
+  unsigned va[2], vb[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = ((lane & 7) ^ ((par << 2) | (lane >> 4))) << 4;
+    va[par] = (unsigned)((lane >> 3) * p.a_rs + chunk);
+    vb[par] = (unsigned)((lane >> 3) * p.b_rs + chunk);
+  }
 
   // fragment offsets: for K step s (16 bf16 = 32 bytes), lane reads chunk 2s + (lane >> 5) of its row
   const int arow0 = wm * (BM / 2) + (lane & 31), brow0 = wn * (BN / 2) + (lane & 31);
   unsigned offa[4], offb[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const unsigned sw = (unsigned)(((2 * s + (lane >> 5)) ^ (lane & 7)) << 4);
+    const unsigned sw = (unsigned)(((2 * s + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
     offa[s] = (unsigned)arow0 * 128u + sw;
     offb[s] = (unsigned)SA + (unsigned)brow0 * 128u + sw;
   }
@@ -100,9 +107,9 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
     for (int q = 0; q < 4; ++q) {
       const unsigned r = (unsigned)((wave * 4 + q) * 8);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * 4 + q) * 1024), 16,
-                                               va + r * (unsigned)p.a_rs, ko, 0, 0);
+                                               va[q & 1] + r * (unsigned)p.a_rs, ko, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * 4 + q) * 1024), 16,
-                                               vb + r * (unsigned)p.b_rs, ko, 0, 0);
+                                               vb[q & 1] + r * (unsigned)p.b_rs, ko, 0, 0);
     }
   };
   auto compute = [&](const u8* stage) {
@@ -182,6 +189,202 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
   }
 }
 
+// ---------------------------------------------------------------- long-K library GEMMs
+//
+// The manifest's library GEMMs at the layer's shapes are long in K and skinny in N: the MoE router (N = 256)
+// and the indexer's weights_proj (N = 32) over M = 16384 rows, K = 6144.  They make few tiles (256 and 128
+// of the batched kernel's 128 x 128), one per CU at most, so a single-stage workgroup leaves every load
+// exposed.  Here one workgroup per CU pipelines its own K loop: a ring of STAGES LDS stages (K = 64 each, the
+// batched kernel's swizzled 128-byte rows), the DMA of stage s + STAGES - 1 issued right after stage s's
+// barrier.  Two shapes:
+//   * wide (N > 64): 128 x 128 tiles, 4 waves of 64 x 64 (TI = TJ = 2); the column tiles of one row block
+//     are consecutive, so they run on one XCD and A comes from HBM once;
+//   * narrow (N <= 64): 64 x 64 tiles, 2 waves of 32 rows x 64 columns (TI = 2, TJ = 1): 256 workgroups at
+//     M = 16384 instead of 128, and the DMA of B rows past n reads nothing.
+// Each output is one chain of v_mfma_f32_32x32x16_bf16 over K in ascending order, as in the batched kernel,
+// so the sums are bit-identical to it.  Every stage index past the last K step is still loaded, from an
+// offset past its resource (reads zeros, touches no memory), so the waits count the same every stage.
+template <bool F32OUT, int BM, int BN, int TI, int TJ, int STAGES>
+__global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void kg_gemm_lib_kernel(const KgBf16Args p) {
+  constexpr int WR = BM / (32 * TJ), WC = BN / (32 * TI), NW = WR * WC;   // waves along rows, columns
+  constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;
+  constexpr int Q = (BM + BN) / 8 / NW;                                 // DMA instructions per wave and stage
+  static_assert((BM + BN) / 8 % NW == 0 && STAGES >= 2, "DMA split");
+  __shared__ __attribute__((aligned(1024))) u8 ring[STAGES * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WR, wn = wave / WR;
+  const int wid = kg_xcd_remap_b((int)blockIdx.x, (int)gridDim.x);
+  const int mt = wid / p.n_tiles, nt = wid - mt * p.n_tiles;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int mv = min(BM, p.m - m0), nv = min(BN, p.n - n0);
+
+  const __amdgpu_buffer_rsrc_t ra = kg_rsrc_b(p.a + (size_t)m0 * p.a_rs, (long long)(mv - 1) * p.a_rs + 2ll * p.k);
+  const __amdgpu_buffer_rsrc_t rb = kg_rsrc_b(p.b + (size_t)n0 * p.b_rs, (long long)(nv - 1) * p.b_rs + 2ll * p.k);
+  // LDS row r keeps 16-byte chunk c in slot c ^ ((r >> 1) & 7): the 16 rows of a ds_read_b128 phase then
+  // cover gfx950's 64 banks once.  A DMA instruction fills 8 rows from a multiple of 8, lane l slot l & 7 of
+  // row l >> 3, so its source chunk depends on the instruction's parity only.
+  unsigned va[2], vb[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = ((lane & 7) ^ ((par << 2) | (lane >> 4))) << 4;
+    va[par] = (unsigned)((lane >> 3) * p.a_rs + chunk);
+    vb[par] = (unsigned)((lane >> 3) * p.b_rs + chunk);
+  }
+
+  const int arow0 = wm * 32 * TJ + (lane & 31), brow0 = wn * 32 * TI + (lane & 31);
+  unsigned offa[4], offb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const unsigned sw = (unsigned)(((2 * s + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
+    offa[s] = (unsigned)arow0 * 128u + sw;
+    offb[s] = (unsigned)SA + (unsigned)brow0 * 128u + sw;
+  }
+
+  v16f acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int KT = p.k >> 6;
+  // stage kt into ring slot `slot`: instruction q of this wave covers LDS rows 8 (wave Q + q) .. + 7 of the
+  // stage (A rows first, then B rows); K steps at or past KT read from past the resource
+  auto issue = [&](int slot, int kt) {
+    const int ko = kt * 128;
+    const unsigned oob = kt < KT ? 0u : 0x80000000u;
+    u8* const stage = ring + slot * STAGE;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int row = (wave * Q + q) * 8;
+      if (row < BM)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + row * 128), 16,
+                                                 (va[q & 1] + (unsigned)row * (unsigned)p.a_rs) | oob, ko, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + row * 128), 16,
+                                                 (vb[q & 1] + (unsigned)(row - BM) * (unsigned)p.b_rs) | oob, ko, 0, 0);
+    }
+  };
+  auto compute = [&](const u8* stage) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      v8bf af[TI], bf[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) af[i] = kg_lds_bf16x8(stage + offb[s] + i * 32 * 128);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) bf[j] = kg_lds_bf16x8(stage + offa[s] + j * 32 * 128);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
+  // stage kt: this wave's DMA of kt has landed (the STAGES - 2 younger stages may still be in flight), the
+  // barrier publishes every wave's and frees slot (kt - 1) % STAGES, into which stage kt + STAGES - 1 goes
+  int slot = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    if constexpr (STAGES == 2) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr ((STAGES - 2) * Q == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr ((STAGES - 2) * Q == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr ((STAGES - 2) * Q == 24) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr ((STAGES - 2) * Q == 32) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr ((STAGES - 2) * Q == 40) asm volatile("s_waitcnt vmcnt(40) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else static_assert(STAGES == 2, "no wait for this ring");
+    asm volatile("" ::: "memory");
+    issue(slot == 0 ? STAGES - 1 : slot - 1, kt + STAGES - 1);
+    compute(ring + slot * STAGE);
+    slot = slot + 1 == STAGES ? 0 : slot + 1;
+  }
+  // the DMA past the last step is still writing (zeros) into the ring: drain it before staging there
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+  if constexpr (F32OUT || BM == 64) {
+    // lane (lane & 31, lane >> 5) holds columns 8 c + 4 (lane >> 5) .. + 3 of row 32 j + (lane & 31) of its
+    // wave's block, c = 4 i + rr: one 16-byte (f32) or 8-byte (bf16) store each
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int r = m0 + wm * 32 * TJ + j * 32 + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int dn = n0 + wn * 32 * TI + (i * 4 + rr) * 8 + (lane >> 5) * 4;
+          if (r < p.m && dn < p.n) {
+            if constexpr (F32OUT) {
+              float4 o;
+              o.x = acc[i][j][rr * 4 + 0], o.y = acc[i][j][rr * 4 + 1], o.z = acc[i][j][rr * 4 + 2];
+              o.w = acc[i][j][rr * 4 + 3];
+              *reinterpret_cast<float4*>(p.d + (size_t)r * p.d_rs + 4 * dn) = o;
+            } else {
+              uint2 o;
+              o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+              o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+              *reinterpret_cast<uint2*>(p.d + (size_t)r * p.d_rs + 2 * dn) = o;
+            }
+          }
+        }
+    }
+  } else {
+    // bf16, 128 x 128 tiles: the batched kernel's LDS-staged epilogue (whole 128-byte row pieces)
+    u8* const stg = ring + wave * 8192;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int m = j * 32 + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = i * 4 + rr;
+          uint2 o;
+          o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + m * 128 + ((c ^ (m & 7)) << 4));
+      const int r = m0 + wm * 64 + m, dn = n0 + wn * 64 + c * 8;
+      if (r < p.m && dn < p.n) *reinterpret_cast<uint4*>(p.d + (size_t)r * p.d_rs + 2 * dn) = v;
+    }
+  }
+}
+
+// The library GEMMs take the long-K kernel from this K on (one stage per 64 of K; below it the batched
+// kernel's many-workgroups-per-CU overlap is enough).
+constexpr int KG_LIB_LONG_K = 1024;
+
+static int kg_gemm_lib_launch(bool f32out, const void* a, const void* b, void* c, int m, int n, int k, long long ldc_b,
+                              void* stream) {
+  KgBf16Args p{};
+  p.a = (const u8*)a, p.b = (const u8*)b, p.d = (u8*)c;
+  p.a_rs = 2ll * k, p.b_rs = 2ll * k, p.d_rs = ldc_b;
+  p.m = m, p.n = n, p.k = k, p.heads = 1, p.hg = 1;
+  const bool wide = n > 64;
+  const int bm = wide ? 128 : 64, bn = wide ? 128 : 64;
+  p.m_tiles = (m + bm - 1) / bm, p.n_tiles = (n + bn - 1) / bn;
+  const long long total = (long long)p.m_tiles * p.n_tiles;
+  KG_CHECK(total < (1ll << 31));
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)total);
+  if (wide) {
+    if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
+  } else {
+    if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 64, 64, 2, 1, 6>), grid, dim3(128), 0, st, p);
+    else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 64, 64, 2, 1, 6>), grid, dim3(128), 0, st, p);
+  }
+  return (int)hipGetLastError();
+}
+
 static int kg_bf16_launch(bool f32out, const void* a, const void* b, void* d, int m, int n, int k, int rows,
                           int heads, long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs,
                           long long d_hs, void* stream) {
@@ -215,11 +418,22 @@ extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int
 // The manifest's library GEMMs (scripts/gen.py:99-102): C[0:m][0:n] = A[m][k] . B[n][k]^T, A and B bf16 row-major
 // with k elements a row, f32 accumulation; C bf16 (gemm_bf16) or f32 (gemm_f32) with ldc elements a row.  One
 // head of the batched kernel.
+// K >= KG_LIB_LONG_K goes to the long-K kernel (same sums, bit for bit).
 extern "C" int kg_gemm_bf16(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream) {
   KG_CHECK(ldc >= n && ldc % 8 == 0);
+  if (k >= KG_LIB_LONG_K && m > 0) {
+    KG_CHECK(a && b && c && n > 0 && n % 8 == 0 && k % 64 == 0 && kg_aligned(a, 16) && kg_aligned(b, 16) &&
+             kg_aligned(c, 16) && 256ll * k < (1ll << 31));
+    return kg_gemm_lib_launch(false, a, b, c, m, n, k, 2ll * ldc, stream);
+  }
   return kg_bf16_launch(false, a, b, c, m, n, k, m, 1, 2ll * k, 0, 2ll * k, 0, 2ll * ldc, 0, stream);
 }
 extern "C" int kg_gemm_bf16_f32(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream) {
   KG_CHECK(ldc >= n && ldc % 4 == 0);
+  if (k >= KG_LIB_LONG_K && m > 0) {
+    KG_CHECK(a && b && c && n > 0 && n % 8 == 0 && k % 64 == 0 && kg_aligned(a, 16) && kg_aligned(b, 16) &&
+             kg_aligned(c, 16) && 256ll * k < (1ll << 31));
+    return kg_gemm_lib_launch(true, a, b, c, m, n, k, 4ll * ldc, stream);
+  }
   return kg_bf16_launch(true, a, b, c, m, n, k, m, 1, 2ll * k, 0, 2ll * k, 0, 4ll * ldc, 0, stream);
 }
