@@ -400,8 +400,8 @@ def cpu_baseline(data, aux, rows=8192, runs=5):
       * dense: fp32 dequantize-then-matmul on rows [0, rows) of each dense GEMM (half the chunk), median of
         `runs` runs: the headline `value`;
       * moe: the m-grouped gate_up and down GEMMs per expert (dequantize-then-matmul of each expert's rows
-        against its weights) over the leading experts of the bench's routing that hold at least 4096 rows;
-      * mqa: the f64 MQA logits of the chunk's last 32 query rows (each against its 65505+ causal keys),
+        against its weights) over the leading experts of the bench's routing that hold at least 8192 rows;
+      * mqa: the f64 MQA logits of the chunk's last 256 query rows (each against its 65281+ causal keys),
         a row at a time as the oracle evaluates it."""
     from oracle import ref
 
@@ -427,7 +427,7 @@ def cpu_baseline(data, aux, rows=8192, runs=5):
 
     m = data["moe"]
     psum = m["psum"].cpu().numpy()
-    G = int(np.searchsorted(psum, 4096)) + 1              # leading experts holding >= 4096 rows
+    G = int(np.searchsorted(psum, 8192)) + 1              # leading experts holding >= 8192 rows
     end = int(psum[G - 1])
     kw1, kw2 = ref.sf_words(H), ref.sf_words(INTER)
     hm = dict(a1=m["mq"][:end].cpu().numpy(), s1=m["msf"].cpu().numpy(), w1=m["w13"][:G * 2 * INTER].cpu().numpy(),
@@ -443,7 +443,7 @@ def cpu_baseline(data, aux, rows=8192, runs=5):
     legs["moe"] = {"value": round(mflops / med / 1e12, 4), "unit": "TFLOP/s", "seconds": round(med, 3),
                    "sample": f"experts 0-{G - 1} ({R} routed rows), gate_up + down"}
 
-    nq = 32
+    nq = 256
     q8, k8 = aux["iq"][-nq:].cpu().numpy(), aux["kg"].cpu().numpy()
     ksf, w = aux["ksf"].cpu().numpy(), aux["w"][-nq:].cpu().numpy()
     ks, ke = aux["ks"][-nq:].cpu().numpy(), aux["ke"][-nq:].cpu().numpy()
