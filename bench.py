@@ -400,7 +400,7 @@ def cpu_baseline(data, aux, rows=8192, runs=5):
       * dense: fp32 dequantize-then-matmul on rows [0, rows) of each dense GEMM (half the chunk), median of
         `runs` runs: the headline `value`;
       * moe: the m-grouped gate_up and down GEMMs per expert (dequantize-then-matmul of each expert's rows
-        against its weights) over the leading experts of the bench's routing that hold at least 8192 rows;
+        against its weights) over the leading experts of the bench's routing up to row slot 8192;
       * mqa: the f64 MQA logits of the chunk's last 256 query rows (each against its 65281+ causal keys),
         a row at a time as the oracle evaluates it."""
     from oracle import ref
@@ -427,7 +427,7 @@ def cpu_baseline(data, aux, rows=8192, runs=5):
 
     m = data["moe"]
     psum = m["psum"].cpu().numpy()
-    G = int(np.searchsorted(psum, 8192)) + 1              # leading experts holding >= 8192 rows
+    G = int(np.searchsorted(psum, 8192)) + 1              # the leading experts up to row slot 8192
     end = int(psum[G - 1])
     kw1, kw2 = ref.sf_words(H), ref.sf_words(INTER)
     hm = dict(a1=m["mq"][:end].cpu().numpy(), s1=m["msf"].cpu().numpy(), w1=m["w13"][:G * 2 * INTER].cpu().numpy(),
