@@ -798,6 +798,43 @@ void kgo_fp8_gemm_mfma(const u8* a, const u8* w, const u8* sfa, const u8* sfb, f
     }
 }
 
+/* The indexer's fp8 MQA logits as the library's kernel evaluates them.  Semantics: the reference's
+   sm100_mqa_logits (source/glm_deepgemm.cu:44-45; scripts/glm_ops.py:101-135):
+     logits[r][j - ks[r]] = sum_{h<32} w[r][h] relu(ksf[j] (q[r][h] . kv[j])),  ks[r] <= j < ke[r].
+   Order (the reference's DeepGEMM order is not public): each dot is two fp8 MFMAs (kgo_mfma_f8, K bytes 0-63
+   with a zero accumulator, then 64-127 onto it, unit scales, the query head as the first operand); per key
+   two f32 chains over the heads {8 i + c} and {8 i + 4 + c} (i < 4, c < 4, in that order), each starting
+   with the product w[h] relu(d) and continuing with fused multiply-adds; their sum times ksf[j] (a power of
+   two, so it leaves the sum exactly as it would the dots).  q e4m3 [num_q][32][128], kv e4m3 [*][128];
+   entries at or past ke - ks are left untouched. */
+void kgo_mqa_logits_mfma(const u8* q, const u8* kv, const float* ksf, const float* w, const long long* ks,
+                         const long long* ke, int num_q, int stride, float* out) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int r = 0; r < num_q; ++r) {
+    const u8* qr = q + (size_t)r * 32 * 128;
+    const float* wr = w + (size_t)r * 32;
+    for (long long j = ks[r]; j < ke[r]; ++j) {
+      const u8* kj = kv + (size_t)j * 128;
+      float d[32];
+      for (int h = 0; h < 32; ++h) {
+        const float lo = kgo_mfma_f8(qr + h * 128, kj, 0.0f, 127, 127);
+        d[h] = kgo_mfma_f8(qr + h * 128 + 64, kj + 64, lo, 127, 127);
+      }
+      float s[2];
+      for (int half = 0; half < 2; ++half) {
+        float acc = 0.0f;
+        for (int e = 0; e < 16; ++e) {
+          const int h = (e >> 2) * 8 + half * 4 + (e & 3);
+          const float x = d[h] > 0.0f ? d[h] : 0.0f;
+          acc = e == 0 ? wr[h] * x : fmaf(wr[h], x, acc);
+        }
+        s[half] = acc;
+      }
+      out[(size_t)r * stride + (j - ks[r])] = (s[0] + s[1]) * ksf[j];
+    }
+  }
+}
+
 /* kgo_mfma_f8 over n independent elements: a, b [n][64], c / out [n], sa / sb [n]. */
 void kgo_mfma_f8_n(const u8* a, const u8* b, const float* c, const int* sa, const int* sb, float* out, long long n) {
 #pragma omp parallel for schedule(static)

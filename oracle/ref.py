@@ -574,6 +574,21 @@ def fp8_gemm_mfma(a, w, sfa, sfb, m, n, k, lda, sfa_rows, sfb_rows=None) -> np.n
     return out
 
 
+def mqa_logits_mfma(q8, k8, ksf, w, ks, ke, num_q, stride) -> np.ndarray:
+    """f32 [num_q][stride]: the MQA logits as the library's kernel evaluates them (kgo_mqa_logits_mfma: fp8
+    MFMA dots, the two fixed head chains, then the key scale); NaN at or past ke - ks."""
+    q8 = np.ascontiguousarray(q8, dtype=np.uint8).reshape(-1)
+    k8 = np.ascontiguousarray(k8, dtype=np.uint8).reshape(-1)
+    ksf = np.ascontiguousarray(ksf, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    ks = np.ascontiguousarray(ks, dtype=np.int64).reshape(-1)
+    ke = np.ascontiguousarray(ke, dtype=np.int64).reshape(-1)
+    out = np.full((num_q, stride), np.nan, np.float32)
+    lib().kgo_mqa_logits_mfma(_p(q8), _p(k8), _p(ksf), _p(w), _p(ks), _p(ke), ctypes.c_int(num_q),
+                              ctypes.c_int(stride), _p(out))
+    return out
+
+
 # ------------------------------------------------------------------ tolerance helpers
 
 def bf16_ulp(x: torch.Tensor) -> torch.Tensor:

@@ -438,16 +438,33 @@ def run_mqa(q8, k8, ksf, w, ks, ke, stride):
     return h(logits, np.float32)
 
 
-def check_mqa(out, q8, k8, ksf, w, ks, ke, stride):
+def check_mqa(out, q8, k8, ksf, w, ks, ke, stride, what="mqa"):
+    """Against the f64 reference: within the f32 summation bound plus the fp8 MFMA's own precision (2^-7 of each
+    64-wide K group's largest product).  Against the oracle's model of the kernel's arithmetic (fp8 MFMA dots,
+    its two head chains, then the key scale): at least 99.9% of the logits equal, the rest within 2^-20 of
+    their |terms| sum (an MFMA output the model misses by an f32 ulp moves one head term).  Nothing is written
+    past a row's key count."""
     num_q = q8.shape[0]
     want = ref.mqa_logits(q8, k8, ksf, w, ks, ke, num_q, stride).numpy()
     S = ref.mqa_logits_abs(q8, k8, ksf, w, ks, ke, num_q, stride).numpy()
     Wn = ref.mqa_logits_window(q8, k8, ksf, w, ks, ke, num_q, stride).numpy()
+    model = ref.mqa_logits_mfma(q8, k8, ksf, w, ks, ke, num_q, stride)
+    n_all = n_eq = 0
+    worst = 0.0
     for r in range(num_q):
         n = int(ke[r] - ks[r])
         err = np.abs(out[r, :n] - want[r, :n])
         assert np.all(err <= 176 * 2.0 ** -24 * S[r, :n] + 2.0 ** -7 * Wn[r, :n] + 1e-30), f"row {r}: worst {err.max()}"
         assert np.all(out[r, n:] == -12345.0), f"row {r} written past its key count"
+        dm = np.abs(out[r, :n].astype(np.float64) - model[r, :n])
+        n_all += n
+        n_eq += int((dm == 0).sum())
+        if n:
+            worst = max(worst, float((dm / (S[r, :n] + 1e-30)).max()))
+    frac = n_eq / max(1, n_all)
+    print(f"PARITY {what}: {n_eq} of {n_all} logits ({frac * 100:.4f}%) equal to the MFMA model, worst "
+          f"|out - model| / sum|terms| {worst:.2e}", flush=True)
+    assert frac >= 0.999 and worst <= 2.0 ** -20, (frac, worst)
 
 
 def test_mqa_logits_bench_shape_sampled():
