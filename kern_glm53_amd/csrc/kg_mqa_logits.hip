@@ -5,14 +5,16 @@
 // ksf[j] * sum_h w[r][h] relu(q_h . k_j), which equals the reference expression in exact arithmetic and
 // rounds only differently in the f32 head summation order.
 //
-// Design: a workgroup of 4 wave64s owns 4 query rows (one per wave, its 32 heads as the rows of the MFMA
+// Design: a workgroup of 8 wave64s owns 8 query rows (one per wave, its 32 heads as the rows of the MFMA
 // tiles, kept in registers for the whole key loop) and walks the union of their key ranges 64 keys at a
 // time.  A key block (64 keys x 128 bytes, and the 64 key scales) is copied HBM -> LDS by
 // buffer_load ... lds into one of two LDS stages (XOR-swizzled rows as in the GEMMs) and consumed as
 // 2 key tiles x 2 K halves of v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales).  Each lane of a 32x32
 // score tile holds one key and 16 of the 32 heads: relu and the head weight (fma) give a partial head
 // sum, v_permlane32_swap pairs the two tiles' halves, one add finishes both tiles' sums, then the key
-// scale and one store of 64 consecutive logits.  18 KB of LDS and 122 VGPRs: 4 workgroups per CU.
+// scale and one store of 64 consecutive logits.  20 KB of LDS and 117 VGPRs: 2 workgroups per CU.  Eight
+// rows per workgroup halve the key traffic into the CUs against four (3.7 against 3.8-4.1 ms at 16384 rows
+// of a 65536-key causal chunk); sixteen, one workgroup per CU, ran 4.2 ms.
 // The file is built with -fno-honor-nans, so fmaxf(x, 0) is one v_max_f32: the scores are finite
 // (products of finite e4m3 codes with unit MFMA scales).
 #include "kg_device.h"
@@ -36,18 +38,18 @@ KG_DEV v8i kg_lds_frag_m(const u8* p0, const u8* p1) {
   return r;
 }
 
-__global__ __launch_bounds__(256, 4) void kg_mqa_logits_kernel(const u8* __restrict__ q, const u8* __restrict__ kv,
+__global__ __launch_bounds__(512, 2) void kg_mqa_logits_kernel(const u8* __restrict__ q, const u8* __restrict__ kv,
                                                                const float* __restrict__ ksf,
                                                                const float* __restrict__ w,
                                                                const unsigned* __restrict__ ks,
                                                                const unsigned* __restrict__ ke,
                                                                float* __restrict__ logits, int num_q, int num_kv,
                                                                int stride) {
-  // a stage: 64 keys x 128 bytes, then 4 regions of 64 key scales (one per wave; region 0 is read)
-  constexpr int BK = 64, TB = BK / 32, KEYB = BK * 128, STAGE = KEYB + 1024;
+  // a stage: 64 keys x 128 bytes, then 8 regions of 64 key scales (one per wave; region 0 is read)
+  constexpr int BK = 64, TB = BK / 32, KEYB = BK * 128, STAGE = KEYB + 2048;
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
-  constexpr int NW = 4, NQ = BK / 8 / NW;          // waves (query rows) per workgroup; key DMAs per wave
+  constexpr int NW = 8, NQ = BK / 8 / NW;          // waves (query rows) per workgroup; key DMAs per wave
   __shared__ unsigned srange[2][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -83,8 +85,8 @@ __global__ __launch_bounds__(256, 4) void kg_mqa_logits_kernel(const u8* __restr
   }
 
   // Key rows are 128 bytes; chunk c of row j sits in slot c ^ ((j >> 1) & 7), so the 16 rows of a
-  // ds_read_b128 phase cover the 64 banks once.  A DMA instruction covers 8 rows starting at 8 (4 wave + qq):
-  // its lanes' swizzle depends on the parity of qq only.  Every row offset is in the VGPR offset, which the
+  // ds_read_b128 phase cover the 64 banks once.  A DMA instruction covers 8 rows starting at 8 (NQ wave + qq):
+  // its lanes' swizzle depends on the parity of NQ wave + qq only.  Every row offset is in the VGPR offset, which the
   // buffer range check covers: keys past num_kv read zeros.
   const __amdgpu_buffer_rsrc_t rkv = kg_rsrc_m(kv, (long long)num_kv * 128);
   const __amdgpu_buffer_rsrc_t rsf = kg_rsrc_m(ksf, (long long)num_kv * 4);
@@ -103,14 +105,14 @@ __global__ __launch_bounds__(256, 4) void kg_mqa_logits_kernel(const u8* __restr
   const __amdgpu_buffer_rsrc_t rlg =
       kg_rsrc_m(logits + (size_t)(live ? r : 0) * stride, live ? (long long)stride * 4 : 0);
 
-  // One block's DMA (3 instructions per wave, the count the waits use): 2 x 8 key rows, and the 64 key
-  // scales (every wave reads them, into its own region; region 0 is the one used).
+  // One block's DMA (NQ + 1 instructions per wave, the count the waits use): NQ x 8 key rows, and the 64
+  // key scales (every wave reads them, into its own region; region 0 is the one used).
   auto issue = [&](u8* stage, unsigned kb) {
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq) {
       const unsigned row = kb + (unsigned)(wave * NQ + qq) * 8u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rkv, (KG_LDS void*)(stage + (wave * NQ + qq) * 1024), 16,
-                                               vk[qq & 1] + row * 128u, 0, 0, 0);
+                                               vk[(wave * NQ + qq) & 1] + row * 128u, 0, 0, 0);
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsf, (KG_LDS void*)(stage + KEYB + wave * 256), 4,
                                              (kb + (unsigned)lane) * 4u, 0, 0, 0);
@@ -153,8 +155,8 @@ __global__ __launch_bounds__(256, 4) void kg_mqa_logits_kernel(const u8* __restr
   v16f acc0[TB], acc1[TB];
   issue(st0, kmin);
   issue(st1, kmin + BK);                         // (past kmax or num_kv: read, never stored)
-  asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
-  static_assert(NQ == 2 && TB == 2, "the waits count 3 DMA instructions and 1 store per block");
+  asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
+  static_assert(NQ == 1 && TB == 2, "the waits count 2 DMA instructions and 1 store per block");
 #pragma unroll
   for (int t = 0; t < TB; ++t) mfma(st0, acc0[t], t);
 
@@ -191,7 +193,7 @@ extern "C" int kg_mqa_logits(const void* q, const void* kv, const float* ksf, co
   // the byte ranges of the key resource and of one logits row (its store offsets are 32-bit)
   KG_CHECK((long long)num_kv * 128 < (1ll << 31) && (long long)stride * 4 < (1ll << 31));
   if (num_q == 0) return 0;
-  hipLaunchKernelGGL(kg_mqa_logits_kernel, dim3((num_q + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(kg_mqa_logits_kernel, dim3((num_q + 7) / 8), dim3(512), 0, (hipStream_t)stream,
                      (const u8*)q, (const u8*)kv, ksf, w, ks, ke, logits, num_q, num_kv, stride);
   return (int)hipGetLastError();
 }
