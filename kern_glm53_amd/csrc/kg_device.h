@@ -4,7 +4,8 @@
 // saturating to +-448 as CUDA's __NV_SATFINITE in the reference, source/glm_glue.cu:76-79 and
 // source/glm_prep.cu:69), the UE8M0 exponent follows source/glm_glue.cu:67-74, and kg_exp is the path's
 // own exp (Cody-Waite reduction, degree-7 Taylor polynomial, explicit fused multiply-adds) evaluated the
-// same way on every device.  The bf16 and packed e4m3 conversions use gfx950's conversion instructions
+// same way on every device.  The SiLU of the MoE's gate values (always bf16) uses the hardware's exp2 and
+// reciprocal instead: a function of the 65536 bf16 inputs, which the tests tabulate on the GPU.  The bf16 and packed e4m3 conversions use gfx950's conversion instructions
 // (v_cvt_pk_bf16_f32, v_cvt_pk_fp8_f32); on a GPU they give the integer rounding below (kg_e4m3) bit for bit
 // on every non-NaN input (bf16: all ties of every bf16 value and 4M random patterns; e4m3: every bf16 value
 // times powers of two within +-448, the only inputs the path produces, as its block scales bound them).
@@ -96,9 +97,20 @@ KG_DEV float kg_exp(float x) {
   return x > 88.72283935546875f ? __builtin_inff() : (x < -103.97208404541015625f ? 0.0f : v);
 }
 
-// SiLU(g) * u rounded to bf16 and back, as source/glm_glue.cu:192 with the path's exp.
+// SiLU(g) = g / (1 + e^-g) for a bf16 gate value g (source/glm_glue.cu:192, whose exp is CUDA's __expf, a
+// hardware exp2 of x log2(e)): e^-g as v_exp_f32 of g * -log2(e), the division as g times v_rcp_f32 of
+// 1 + e^-g.  Five instructions, two of them transcendental, against about 27 for the Cody-Waite exp and an
+// IEEE division; within (|g| log2(e) + 4) f32 ulp of the exact value (the rounding of g * log2(e) scales
+// with |g|, as the reference's __expf error does).  The result depends only on g's 16 bits, so the tests
+// pin the function as a committed table of its 65536 values, generated on the GPU by this code.
+KG_DEV float kg_silu_f32(float g) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896340736f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// SiLU(g) * u rounded to bf16 and back (source/glm_glue.cu:192).
 KG_DEV float kg_silu_mul_bf16(float g, float u) {
-  return kg_bf16_to_f32(kg_f32_to_bf16(g / (1.0f + kg_exp(-g)) * u));
+  return kg_bf16_to_f32(kg_f32_to_bf16(kg_silu_f32(g) * u));
 }
 
 // This lane's id within the wave (v_mbcnt), formed where it is used: the empty asm makes the value opaque,

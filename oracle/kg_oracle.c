@@ -8,6 +8,7 @@
  * Compiled with -ffp-contract=off so that every fused multiply-add below is an explicit fmaf().
  */
 #include <math.h>
+#include <stdio.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -75,7 +76,7 @@ u8 kgo_ue8m0(float amax, float eps, float* scale) {
 
 /* The path's exp: 2^n * e^r with n = rint(x * log2 e), r = x - n ln2 (Cody-Waite two-constant split,
  * fused), e^r by its degree-7 Taylor polynomial in Horner form, then ldexp.  The HIP kernels evaluate
- * the same operations in the same order, so SiLU and the router's sigmoid agree bit for bit. */
+ * the same operations in the same order, so the router's sigmoid agrees bit for bit. */
 float kgo_exp(float x) {
   if (x > 88.72283935546875f) return INFINITY;
   if (x < -103.97208404541015625f) return 0.0f;
@@ -116,17 +117,32 @@ void kgo_quant(const u16* x, int ldx, u8* q, u8* sf, int sf_rows, int K, int T) 
     }
 }
 
-/* glm_silu_mul_quant, glm_glue.cu:177-194: act = bf16(g / (1 + exp(-g)) * u) over the gate | up halves
- * of gu [rows][2I], quantized per 128 columns.  Rows at or past *n (when n is given) are skipped. */
+/* SiLU(g) = g / (1 + e^-g) of a bf16 gate value, glm_glue.cu:192.  The reference's e^-g is CUDA's __expf, a
+ * hardware exp2 approximation; the HIP kernels use gfx950's v_exp_f32 and v_rcp_f32, whose exact values are
+ * not specified, so SiLU is taken from the table of its 65536 values (indexed by g's bf16 bits) that the
+ * library's own device function produced on the GPU (tests/golden/silu_f32_bf16.npz, set by the caller;
+ * pinned within (|g| log2(e) + 4) ulp of the exact SiLU). */
+static const float* kgo_silu_tab = 0;
+void kgo_set_silu_table(const float* t) { kgo_silu_tab = t; }
+float kgo_silu(u16 g_bits) {
+  if (!kgo_silu_tab) {
+    fprintf(stderr, "kgo_silu: no SiLU table set (kgo_set_silu_table)\n");
+    abort();
+  }
+  return kgo_silu_tab[g_bits];
+}
+
+/* glm_silu_mul_quant, glm_glue.cu:177-194: act = bf16(silu(g) * u) over the gate | up halves of gu
+ * [rows][2I], quantized per 128 columns.  Rows at or past *n (when n is given) are skipped. */
 void kgo_silu_mul_quant(const u16* gu, int I, u8* q, u8* sf, int sf_rows, const int* n, int rows) {
   float v[128];
   const int live = n ? (*n < rows ? *n : rows) : rows;
   for (int r = 0; r < live; ++r)
     for (int kb = 0; kb < I / 128; ++kb) {
       for (int i = 0; i < 128; ++i) {
-        const float g = kgo_bf16_to_f32(gu[(size_t)r * 2 * I + kb * 128 + i]);
+        const u16 gb = gu[(size_t)r * 2 * I + kb * 128 + i];
         const float u = kgo_bf16_to_f32(gu[(size_t)r * 2 * I + I + kb * 128 + i]);
-        v[i] = kgo_bf16_to_f32(kgo_f32_to_bf16(g / (1.0f + kgo_exp(-g)) * u));
+        v[i] = kgo_bf16_to_f32(kgo_f32_to_bf16(kgo_silu(gb) * u));
       }
       quant_block(v, q + (size_t)r * I + kb * 128, sf, sf_rows, r, kb, 1e-10f);
     }

@@ -43,12 +43,29 @@ def build() -> pathlib.Path:
     return LIB_PATH
 
 
+SILU_TABLE = HERE.parent / "tests" / "golden" / "silu_f32_bf16.npz"
+_silu = None
+
+
+def silu_table() -> np.ndarray:
+    """The library's SiLU of every bf16 gate value, f32 [65536] indexed by the bf16 bits (tabulated on the GPU by
+    tests/golden/make_silu_table.py; pinned against float64 SiLU in tests/test_oracle_silu.py)."""
+    global _silu
+    if _silu is None:
+        t = np.ascontiguousarray(np.load(SILU_TABLE)["silu"], dtype=np.float32)
+        assert t.shape == (65536,), t.shape
+        _silu = t
+    return _silu
+
+
 def lib():
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        _lib = ctypes.CDLL(str(LIB_PATH))
+        l = ctypes.CDLL(str(LIB_PATH))
+        l.kgo_set_silu_table(ctypes.c_void_p(silu_table().ctypes.data))   # the array stays referenced in _silu
+        _lib = l
     return _lib
 
 

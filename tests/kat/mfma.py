@@ -15,30 +15,47 @@ import subprocess
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-SRC = HERE / "kg_mfma_kat.hip"
+SRCS = [HERE / "kg_mfma_kat.hip", HERE / "kg_silu_kat.hip"]
 LIB = HERE / "libkgkat.so"
+CSRC = HERE.parents[1] / "kern_glm53_amd" / "csrc"
 
 
 def build() -> pathlib.Path:
-    cmd = ["hipcc", "-O2", "-std=c++17", "-shared", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature",
-           "-Xclang", "-packed-fp32-ops", str(SRC), "-o", str(LIB)]
+    """Both harness kernels, with the library's compile flags for its device helpers (kg_device.h)."""
+    cmd = ["hipcc", "-O3", "-std=c++17", "-shared", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", "-ffp-contract=off", f"-I{CSRC}", *map(str, SRCS), "-o", str(LIB)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
-        raise RuntimeError(f"hipcc failed on {SRC}:\n{r.stderr}")
+        raise RuntimeError(f"hipcc failed on {SRCS}:\n{r.stderr}")
     return LIB
 
 
 _lib = None
 
 
-def run(a, b, c, sa, sb) -> np.ndarray:
-    """Runs the cases on cuda:0; returns d f32 [cases][64][16]."""
-    import torch
+def _harness():
     global _lib
     if _lib is None:
         if not LIB.exists():
             raise RuntimeError(f"{LIB} is not built (tests/kat/mfma.build())")
         _lib = ctypes.CDLL(str(LIB))
+    return _lib
+
+
+def silu_table() -> np.ndarray:
+    """The library's SiLU (kg_silu_f32) on cuda:0 for every bf16 bit pattern: f32 [65536]."""
+    import torch
+    out = torch.empty(65536, dtype=torch.float32, device=torch.device("cuda:0"))
+    rc = _harness().kg_silu_kat(ctypes.c_void_p(out.data_ptr()), None)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def run(a, b, c, sa, sb) -> np.ndarray:
+    """Runs the cases on cuda:0; returns d f32 [cases][64][16]."""
+    import torch
+    _lib = _harness()
     dev = torch.device("cuda:0")
     n = a.shape[0]
     t = [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (a, b, c, sa.astype(np.int32), sb.astype(np.int32))]

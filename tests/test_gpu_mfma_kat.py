@@ -2,7 +2,8 @@
 the instruction under every fp8 GEMM of the library, through the harness in tests/kat: the probes' outputs
 (each pins one rule of the instruction's truncation and rounding) and seeded random cases, against the
 oracle's model of it (oracle/kg_oracle.c kgo_mfma_f8) and against the outputs committed in
-tests/golden/mfma_f8_kat.npz."""
+tests/golden/mfma_f8_kat.npz; and the library's SiLU (kg_silu_f32) against the table the oracle uses
+(tests/golden/silu_f32_bf16.npz)."""
 import pathlib
 
 import numpy as np
@@ -52,3 +53,11 @@ def test_committed_outputs_reproduce():
     f = np.load(FIX)
     hw = mfma.run(f["rand_a"], f["rand_b"], f["rand_c"], f["rand_sa"], f["rand_sb"])
     assert np.array_equal(hw.view(np.uint32), f["rand_d"].view(np.uint32))
+
+
+def test_silu_table_reproduces():
+    """The library's SiLU (kg_silu_f32, v_exp_f32 and v_rcp_f32) evaluated now on every bf16 gate value equals the
+    committed table the oracle looks SiLU up in, bit for bit."""
+    print("silu kat: 65536 bf16 inputs", flush=True)
+    hw = mfma.silu_table()
+    assert np.array_equal(hw.view(np.uint32), ref.silu_table().view(np.uint32))
