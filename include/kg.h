@@ -79,8 +79,10 @@ int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, 
 /* The manifest's library GEMMs, `gemm_bf16` (extern:cublaslt_bf16_tn) and `gemm_f32` (extern:cublas_bf16_tn_f32),
  * scripts/gen.py:99-102; used by the indexer's weights_proj (gen.py:368) and the MoE router (gen.py:435):
  * C[0:m][0:n] = A . B^T, A bf16 [m][k], B bf16 [n][k] (both row-major, k elements a row), f32 accumulation,
- * C bf16 (kg_gemm_bf16) or f32 (kg_gemm_bf16_f32) with ldc elements a row.  One head of kg_bf16_batched's
- * kernel.  Requires k % 64 == 0, n % 8 == 0, 16-byte aligned pointers, ldc % 8 == 0 (bf16) or % 4 (f32). */
+ * C bf16 (kg_gemm_bf16) or f32 (kg_gemm_bf16_f32) with ldc elements a row.  Below k = 1024 one head of
+ * kg_bf16_batched's kernel; from k = 1024 a multi-stage ring kernel (n > 64) or a kernel splitting K over its
+ * waves (n <= 64).  Deterministic.  Requires k % 64 == 0, n % 8 == 0, 16-byte aligned pointers, ldc % 8 == 0
+ * (bf16) or % 4 (f32). */
 int kg_gemm_bf16(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream);
 int kg_gemm_bf16_f32(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream);
 

@@ -196,11 +196,8 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
 // of the batched kernel's 128 x 128), one per CU at most, so a single-stage workgroup leaves every load
 // exposed.  Here one workgroup per CU pipelines its own K loop: a ring of STAGES LDS stages (K = 64 each, the
 // batched kernel's swizzled 128-byte rows), the DMA of stage s + STAGES - 1 issued right after stage s's
-// barrier.  Two shapes:
-//   * wide (N > 64): 128 x 128 tiles, 4 waves of 64 x 64 (TI = TJ = 2); the column tiles of one row block
-//     are consecutive, so they run on one XCD and A comes from HBM once;
-//   * narrow (N <= 64): 64 x 64 tiles, 2 waves of 32 rows x 64 columns (TI = 2, TJ = 1): 256 workgroups at
-//     M = 16384 instead of 128, and the DMA of B rows past n reads nothing.
+// barrier; 128 x 128 tiles, 4 waves of 64 x 64 (TI = TJ = 2); the column tiles of one row block are
+// consecutive, so they run on one XCD and A comes from HBM once.  (N <= 64 takes kg_gemm_ksplit_kernel below.)
 // Each output is one chain of v_mfma_f32_32x32x16_bf16 over K in ascending order, as in the batched kernel,
 // so the sums are bit-identical to it.  Every stage index past the last K step is still loaded, from an
 // offset past its resource (reads zeros, touches no memory), so the waits count the same every stage.
@@ -328,7 +325,7 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
   // the DMA past the last step is still writing (zeros) into the ring: drain it before staging there
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 
-  if constexpr (F32OUT || BM == 64) {
+  if constexpr (F32OUT) {
     // lane (lane & 31, lane >> 5) holds columns 8 c + 4 (lane >> 5) .. + 3 of row 32 j + (lane & 31) of its
     // wave's block, c = 4 i + rr: one 16-byte (f32) or 8-byte (bf16) store each
 #pragma unroll
@@ -382,9 +379,166 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
   }
 }
 
-// The library GEMMs take the long-K kernel from this K on (one stage per 64 of K; below it the batched
+// Narrow library GEMMs (N <= 64: the indexer's weights_proj, N = 32, over M = 16384 rows, K = 6144): almost
+// all of the traffic is A, read once, and the matrix work is small, so the kernel is a stream of A.  A workgroup
+// of 4 waves owns BM rows x all BN columns and splits K between its waves: wave w takes K steps
+// [w KT / 4, (w + 1) KT / 4) (64 each) through its own ring of S LDS stages (the swizzled 128-byte rows; BM A
+// rows, then BN B rows), so the waves never wait for each other inside the loop (each waits for its own DMA
+// only).  That gives M / BM workgroups of 4 independent streams (512 / 256 at M = 16384) where the 64 x 64 tile
+// kernel had 256 workgroups of 2 waves in lockstep.  At the end each wave leaves its BM x BN partial sums
+// (f32) in its ring, and every output is the four partials added in wave order, ((p0 + p1) + p2) + p3, so the
+// result does not depend on timing; the f32 and bf16 variants share the sums (bf16 rounds the same f32).
+template <bool F32OUT, int BM, int BN, int S>
+__global__ __launch_bounds__(256, 1) void kg_gemm_ksplit_kernel(const KgBf16Args p) {
+  constexpr int NW = 4, ROWS = BM + BN, Q = ROWS / 8, STAGE = ROWS * 128, RING = S * STAGE;
+  constexpr int TJ = BM / 32, TI = BN / 32;
+  static_assert(BM * BN * 4 <= RING && S >= 2 && (S - 2) * Q <= 48, "ring sizes");
+  static_assert(BM * BN / 8 % 256 == 0, "the reduction gives every thread whole passes of 8 columns");
+  __shared__ __attribute__((aligned(1024))) u8 lds[NW * RING];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the column tiles of one row block are consecutive, so they run on one XCD and share A in its L2
+  const int wid = kg_xcd_remap_b((int)blockIdx.x, (int)gridDim.x);
+  const int mt = wid / p.n_tiles, nt = wid - mt * p.n_tiles;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int mv = min(BM, p.m - m0), nv = min(BN, p.n - n0);
+  const __amdgpu_buffer_rsrc_t ra = kg_rsrc_b(p.a + (size_t)m0 * p.a_rs, (long long)(mv - 1) * p.a_rs + 2ll * p.k);
+  const __amdgpu_buffer_rsrc_t rb = kg_rsrc_b(p.b + (size_t)n0 * p.b_rs, (long long)(nv - 1) * p.b_rs + 2ll * p.k);
+  const int KT = p.k >> 6, k0 = wave * KT / NW, k1 = (wave + 1) * KT / NW, nk = k1 - k0;
+  u8* const ring = lds + wave * RING;
+
+  unsigned va[2], vb[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int chunk = ((lane & 7) ^ ((par << 2) | (lane >> 4))) << 4;
+    va[par] = (unsigned)((lane >> 3) * p.a_rs + chunk);
+    vb[par] = (unsigned)((lane >> 3) * p.b_rs + chunk);
+  }
+  unsigned off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    off[s] = (unsigned)(lane & 31) * 128u + (unsigned)(((2 * s + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
+
+  // DMA instruction q of K step kt into ring slot `slot` (rows 8 q .. 8 q + 7 of the stage: A rows, then B
+  // rows); steps past this wave's range read zeros from past the resource
+  auto issue1 = [&](int slot, int kt, int q) {
+    const int ko = kt * 128;
+    const unsigned oob = kt < k1 ? 0u : 0x80000000u;
+    u8* const st = ring + slot * STAGE + q * 1024;
+    if (q < BM / 8)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)st, 16,
+                                               (va[q & 1] + (unsigned)(q * 8) * (unsigned)p.a_rs) | oob, ko, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)st, 16,
+                                               (vb[q & 1] + (unsigned)(q * 8 - BM) * (unsigned)p.b_rs) | oob, ko, 0, 0);
+  };
+
+  v16f acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+#pragma unroll
+    for (int q = 0; q < Q; ++q) issue1(s, k0 + s, q);
+  int slot = 0;
+  for (int t = 0; t < nk; ++t) {
+    // this wave's DMA of step t has landed (the S - 2 younger steps may still be in flight)
+    if constexpr ((S - 2) * Q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr ((S - 2) * Q == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if constexpr ((S - 2) * Q == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else if constexpr ((S - 2) * Q == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if constexpr ((S - 2) * Q == 24) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if constexpr ((S - 2) * Q == 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+    else static_assert((S - 2) * Q == 0, "no wait for this ring");
+    const u8* const st = ring + slot * STAGE;
+    v8bf af[4][TJ], bf[4][TI];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) af[s][j] = kg_lds_bf16x8(st + off[s] + j * 32 * 128);
+#pragma unroll
+      for (int i = 0; i < TI; ++i) bf[s][i] = kg_lds_bf16x8(st + BM * 128 + off[s] + i * 32 * 128);
+    }
+    // the slot of step t - 1 (its reads are done: its MFMAs have run) takes step t + S - 1
+    const int nslot = slot == 0 ? S - 1 : slot - 1;
+    constexpr int NM = 4 * TI * TJ;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[s][i], af[s][j], acc[i][j], 0, 0, 0);
+          const int m = (s * TI + i) * TJ + j;
+#pragma unroll
+          for (int q = 0; q < Q; ++q)
+            if (q * NM / Q == m) issue1(nslot, k0 + t + S - 1, q);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    slot = slot + 1 == S ? 0 : slot + 1;
+  }
+  // the trailing zero DMA into the ring has landed, and every wave's reads are done, before the partials go there
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // lane (lane & 31, lane >> 5) of MFMA tile (i, j) holds columns 32 i + 8 rr + 4 (lane >> 5) .. + 3 of row
+  // 32 j + (lane & 31)
+  float* const part = reinterpret_cast<float*>(ring);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j)
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int r = 32 * j + (lane & 31), c = 32 * i + 8 * rr + 4 * (lane >> 5);
+        *reinterpret_cast<float4*>(part + r * BN + c) =
+            make_float4(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1], acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+      }
+  __syncthreads();
+  // thread: row tid / (BN / 8)... 8 consecutive columns per pass
+  constexpr int CPR = BN / 8, PASSES = BM * CPR / 256;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int x = ps * 256 + tid, r = x / CPR, c = (x % CPR) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float* const src = reinterpret_cast<const float*>(lds + w * RING) + r * BN + c;
+      const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+      if (w == 0) {
+        v[0] = lo.x, v[1] = lo.y, v[2] = lo.z, v[3] = lo.w, v[4] = hi.x, v[5] = hi.y, v[6] = hi.z, v[7] = hi.w;
+      } else {
+        v[0] += lo.x, v[1] += lo.y, v[2] += lo.z, v[3] += lo.w, v[4] += hi.x, v[5] += hi.y, v[6] += hi.z, v[7] += hi.w;
+      }
+    }
+    if (r < mv && c < nv) {
+      u8* const dst = p.d + (size_t)(m0 + r) * p.d_rs + (F32OUT ? 4 : 2) * (size_t)n0;
+      if constexpr (F32OUT) {
+        *reinterpret_cast<float4*>(dst + 4 * c) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(dst + 4 * c + 16) = make_float4(v[4], v[5], v[6], v[7]);
+      } else {
+        uint4 o;
+        o.x = kg_pack_bf16x2(v[0], v[1]), o.y = kg_pack_bf16x2(v[2], v[3]);
+        o.z = kg_pack_bf16x2(v[4], v[5]), o.w = kg_pack_bf16x2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(dst + 2 * c) = o;
+      }
+    }
+  }
+}
+
+// The library GEMMs take the long-K kernels from this K on (one stage per 64 of K; below it the batched
 // kernel's many-workgroups-per-CU overlap is enough).
 constexpr int KG_LIB_LONG_K = 1024;
+// Up to N = 64 they take the K-split stream kernel (64-row workgroups; rings of 3 stages for N <= 32, 2 for
+// N <= 64, within the 160 KB of LDS).  Wider N (the router's 256) keeps the 128 x 128 ring kernel: the K-split
+// kernel over 64-column tiles ran it at 97 us against 91.
+constexpr int KG_KSPLIT_MAX_N = 64, KG_KSPLIT_BM = 64, KG_KSPLIT_S32 = 3, KG_KSPLIT_S64 = 2;
 
 static int kg_gemm_lib_launch(bool f32out, const void* a, const void* b, void* c, int m, int n, int k, long long ldc_b,
                               void* stream) {
@@ -392,20 +546,29 @@ static int kg_gemm_lib_launch(bool f32out, const void* a, const void* b, void* c
   p.a = (const u8*)a, p.b = (const u8*)b, p.d = (u8*)c;
   p.a_rs = 2ll * k, p.b_rs = 2ll * k, p.d_rs = ldc_b;
   p.m = m, p.n = n, p.k = k, p.heads = 1, p.hg = 1;
-  const bool wide = n > 64;
-  const int bm = wide ? 128 : 64, bn = wide ? 128 : 64;
-  p.m_tiles = (m + bm - 1) / bm, p.n_tiles = (n + bn - 1) / bn;
+  hipStream_t st = (hipStream_t)stream;
+  if (n <= KG_KSPLIT_MAX_N) {
+    // the K-split stream kernel: BM rows x 32 or 64 columns per workgroup
+    constexpr int BM = KG_KSPLIT_BM;
+    const int bn = n <= 32 ? 32 : 64;
+    p.m_tiles = (m + BM - 1) / BM, p.n_tiles = (n + bn - 1) / bn;
+    KG_CHECK((long long)p.m_tiles * p.n_tiles < (1ll << 31));
+    const dim3 grid((unsigned)(p.m_tiles * p.n_tiles));
+    if (n <= 32) {
+      if (f32out) hipLaunchKernelGGL((kg_gemm_ksplit_kernel<true, BM, 32, KG_KSPLIT_S32>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((kg_gemm_ksplit_kernel<false, BM, 32, KG_KSPLIT_S32>), grid, dim3(256), 0, st, p);
+    } else {
+      if (f32out) hipLaunchKernelGGL((kg_gemm_ksplit_kernel<true, BM, 64, KG_KSPLIT_S64>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((kg_gemm_ksplit_kernel<false, BM, 64, KG_KSPLIT_S64>), grid, dim3(256), 0, st, p);
+    }
+    return (int)hipGetLastError();
+  }
+  p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
   const long long total = (long long)p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
-  hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)total);
-  if (wide) {
-    if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
-  } else {
-    if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 64, 64, 2, 1, 6>), grid, dim3(128), 0, st, p);
-    else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 64, 64, 2, 1, 6>), grid, dim3(128), 0, st, p);
-  }
+  if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
@@ -442,7 +605,8 @@ extern "C" int kg_bf16_batched(const void* a, const void* b, void* d, int m, int
 // The manifest's library GEMMs (scripts/gen.py:99-102): C[0:m][0:n] = A[m][k] . B[n][k]^T, A and B bf16 row-major
 // with k elements a row, f32 accumulation; C bf16 (gemm_bf16) or f32 (gemm_f32) with ldc elements a row.  One
 // head of the batched kernel.
-// K >= KG_LIB_LONG_K goes to the long-K kernel (same sums, bit for bit).
+// K >= KG_LIB_LONG_K goes to the long-K kernels: for N > 64 the same sums as the batched kernel, bit for bit;
+// for N <= 64 the K-split kernel's (four K quarters added in a fixed order).
 extern "C" int kg_gemm_bf16(const void* a, const void* b, void* c, int m, int n, int k, int ldc, void* stream) {
   KG_CHECK(ldc >= n && ldc % 8 == 0);
   if (k >= KG_LIB_LONG_K && m > 0) {
