@@ -79,20 +79,47 @@ KG_DEV u32 kg_or8(u32 v) {
   return v;
 }
 
-// One radix pass: histogram of the candidates' next wd bits (candidates: (key & m) == pm) fed by `feed`,
-// which calls its argument on every key; then the bin holding the need-th largest.  Updates pm, m, s, need
-// and sets cnt to that bin's count.
-template <class Feed>
+// One radix pass: histogram of the candidates' next wd bits (candidates: (key & m) == pm), fed by `feed`,
+// which calls its argument on every group of 8 keys; then the bin holding the need-th largest.  Updates pm,
+// m, s, need and sets cnt to that bin's count.  S2 / WD >= 0 fix the pass's bit field at compile time (the
+// passes of a row held in registers: bits 21-31, 10-20, 0-9), so the extract takes immediate operands.
+// ALL: every key is a candidate (the first pass, m = 0): no test, one extract, one address and the LDS add
+// per key.  Otherwise a group of 8 keys none of which is a candidate in any lane of the wave (most groups
+// once the earlier passes have narrowed the candidates to one bin) costs 8 compares and one scalar branch.
+struct KgKeys8 {
+  u32 v[8];
+};
+template <bool ALL, int S2, int WD, class Feed>
 KG_DEV void kg_tk_pass(Feed feed, u32* lds, int* wsum, int* found, u32& pm, u32& m, int& s, int& need, int& cnt) {
   const int t = threadIdx.x, lane = t & 63;
-  const int wd = min(11, s), s2 = s - wd, NB = 1 << wd;
+  const int wd = WD >= 0 ? WD : min(11, s), s2 = S2 >= 0 ? S2 : s - wd, NB = 1 << wd;
   for (int i = t; i < 4 * NB; i += KG_TK_T) lds[i] = 0;
   __syncthreads();
-  const u32 m0 = m, pm0 = pm;
-  feed([&](u32 k) {
-    if ((k & m0) == pm0)
-      __hip_atomic_fetch_add(&lds[(((k >> s2) & (u32)(NB - 1)) << 2) | (u32)(lane & 3)], 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_WORKGROUP);
+  const u32 m0 = m, pm0 = pm, sub = (u32)(lane & 3);
+  auto add = [&](u32 k) {
+    u32 b;
+    if constexpr (S2 >= 0) b = (k >> S2) & ((1u << WD) - 1u);
+    else b = (k >> s2) & (u32)(NB - 1);
+    __hip_atomic_fetch_add(&lds[(b << 2) | sub], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  feed([&](const KgKeys8& g) {
+    if constexpr (ALL) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) add(g.v[e]);
+    } else {
+      // the group's candidates in the whole wave, read back as a uniform value so that the test stays a
+      // scalar branch (a lane's candidate implies a nonzero mask, which would otherwise fold the test into
+      // the lane mask)
+      unsigned long long bal = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bal |= __builtin_amdgcn_ballot_w64((g.v[e] & m0) == pm0);
+      const u32 any = __builtin_amdgcn_readfirstlane((u32)bal) | __builtin_amdgcn_readfirstlane((u32)(bal >> 32));
+      if (any != 0u) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if ((g.v[e] & m0) == pm0) add(g.v[e]);
+      }
+    }
   });
   __syncthreads();
   // descending bins: thread t sums bins NB-1-2t and NB-2-2t (NB is even)
@@ -188,7 +215,12 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
     for (int seg = 0; seg < nseg; ++seg) {
       if (MULTI) load(seg);
 #pragma unroll
-      for (int j = 0; j < KG_TK_V; ++j) f(key[j]);
+      for (int j = 0; j < KG_TK_V; j += 8) {
+        KgKeys8 g;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g.v[e] = key[j + e];
+        f(g);
+      }
     }
   };
   // taken / equal bits of this thread's elements into the two bitmaps: thread t's nibble of elements
@@ -222,7 +254,10 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
     // smallest and largest valid key: the bits above their first difference are common to every
     // candidate, which can save a pass over the re-read segments
     u32 kmin = 0xffffffffu, kmax = 0u;
-    feed_regs([&](u32 k) { kmin = min(kmin, k ? k : 0xffffffffu), kmax = max(kmax, k); });
+    feed_regs([&](const KgKeys8& g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kmin = min(kmin, g.v[e] ? g.v[e] : 0xffffffffu), kmax = max(kmax, g.v[e]);
+    });
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
       kmin = min(kmin, (u32)__shfl_xor((int)kmin, o, 64));
@@ -246,13 +281,15 @@ __global__ __launch_bounds__(KG_TK_T) void kg_topk_kernel(const float* __restric
     // 1.9 with the bin found by one wave instead of a block-wide scan, and 2.1 with the first pass's bin
     // compacted into an LDS list for one wave to finish.
     load(0);
-    while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    kg_tk_pass<true, 21, 11>(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    if (cnt != need) kg_tk_pass<false, 10, 11>(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    if (cnt != need) kg_tk_pass<false, 0, 10>(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
     const bool ties = cnt > need;
     mark(m, pm, !ties, ties);
     int eq_base = 0, out_base = 0;
     kg_tk_emit(taken, eqbm, ties, need, eq_base, out_base, wsum, orow, 0, lo);
   } else {
-    while (cnt != need && s > 0) kg_tk_pass(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
+    while (cnt != need && s > 0) kg_tk_pass<false, -1, -1>(feed_regs, lds, wsum, found, pm, m, s, need, cnt);
     const bool ties = cnt > need;
     int eq_base = 0, out_base = 0;
     for (int seg = 0; seg < nseg; ++seg) {
