@@ -113,13 +113,15 @@ KG_DEV float kg_silu_mul_bf16(float g, float u) {
   return kg_bf16_to_f32(kg_f32_to_bf16(kg_silu_f32(g) * u));
 }
 
-// This lane's id within the wave (v_mbcnt), formed where it is used: the empty asm makes the value opaque,
-// so address arithmetic built on it is not hoisted out of a loop into registers the loop needs.  The
-// v_mbcnt instructions themselves are the compiler's, so its hazard checks see them.
+// This lane's id within the wave (v_mbcnt), formed where it is used: the count starts from a zero that an
+// empty volatile asm produces at the call, so neither the v_mbcnt pair nor the address arithmetic built on
+// it can be hoisted out of a loop into a register held across it (with every register taken, such a value
+// is spilled, and its reload waits for all vector memory in flight).  The v_mbcnt instructions themselves
+// are the compiler's, so its hazard checks see them.
 KG_DEV int kg_lane_here() {
-  int l = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-  asm volatile("" : "+v"(l));
-  return l;
+  unsigned z = 0;
+  asm volatile("" : "+v"(z));
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z));
 }
 
 // Max over groups of `width` consecutive lanes (width a power of two <= 64).

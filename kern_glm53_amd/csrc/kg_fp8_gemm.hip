@@ -412,8 +412,8 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
 // contiguous bytes per lane and 8 lanes cover a 128-byte row segment (a whole line).  `stage` is the wave's
 // own 4 KB: each 32-row MFMA tile j goes through it in two rounds of 64 columns (n tiles 2 ch, 2 ch + 1), all
 // 64 lanes writing their rows' 8-byte pieces (chunk c of 8 columns of row m in slot c ^ (m & 7)), then
-// reading 16-byte chunks back.  Every wave issues exactly 32 stores per tile, which the next tile's first
-// barrier leaves in flight.  The stores are non-temporal (the kernel never reads its outputs back; o_proj ran
+// reading 16-byte chunks back.  Every wave issues exactly 32 stores per tile, which drain during the next
+// tile's first stage (its barrier waits for them).  The stores are non-temporal (the kernel never reads its outputs back; o_proj ran
 // 2.7% faster).  Against rounds of 16 rows x 128 columns (half the lanes writing, 256-byte row segments) this
 // took q_b from 0.465 to 0.451 ms.  Storing from the registers instead (v_permlane32_swap pairs, 32 bytes per
 // row per instruction) skipped the staging but ran q_b at 0.86 ms: whole-line row segments matter most.
@@ -486,7 +486,9 @@ KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stag
         acc[i][j][r] = v;                        // the product overwrites the gate accumulator
         am = fmaxf(am, fabsf(v));
       }
-    am = fmaxf(am, __shfl_xor(am, 32, 64));
+    // the other half-wave's value (lane ^ 32), addressed from this call's lane id: __shfl_xor's own lane id
+    // would be formed once, before the tile loop, and held (spilled) across it
+    am = fmaxf(am, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, am))));
     if (lane < 32) xam[wn][arow0 + j * 32] = am;
   }
   // LDS-only barriers: the vector-memory queue (the next tile's DMA in flight) is not waited on
@@ -669,13 +671,23 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     } else {
       unsigned u = q < 8 ? (d.half && wave >= 2 ? KG_OOB : arow_w + d.abase) : wrow_w + d.wbase;
       if (ko >= p.k) u = KG_OOB;
-      // The row step and the lane offset pass through an empty asm statement, so that the compiler forms the
-      // VGPR offset here rather than keeping 16 precomputed offsets per buffer in registers; the
-      // instruction's immediate offset (added to both the LDS and the memory address) places instructions
-      // j & 3, so only 4 LDS bases per buffer remain.
+      // The lane offset passes through an empty asm statement, so that the compiler forms the VGPR offset
+      // here rather than keeping 16 precomputed offsets per buffer in vector registers.  The row term
+      // j * 8 lda (8 k) is vector work in modes 0 and 2 (from a zero the asm also yields) and scalar work in
+      // mode 1: each measured the faster form for that mode (dense and gate_up shapes 1-2% apart, the
+      // MoE down GEMM 3%).  A vector copy of the row step held across the tile loop instead gets spilled to
+      // scratch.  The instruction's immediate offset (added to both the LDS and the memory address) places
+      // instructions j & 3, so only 4 LDS bases per buffer remain.
       v = q < 8 ? va[j & 1] : vw[j & 1];
-      unsigned rs = 8u * (unsigned)(q < 8 ? p.lda : p.k);
-      asm volatile("" : "+v"(v), "+v"(rs));
+      unsigned rs;
+      if constexpr (MODE != 1) {
+        unsigned z = 0;
+        asm volatile("" : "+v"(v), "+v"(z));
+        rs = 8u * (unsigned)(q < 8 ? p.lda : p.k) + z;
+      } else {
+        rs = 8u * (unsigned)(q < 8 ? p.lda : p.k);
+        asm volatile("" : "+v"(v));
+      }
       v += u + (unsigned)j * rs - (unsigned)((j & 3) * 1024);
     }
     u8* const m0 = st + (q < 8 ? 0 : SA) + wave * 8192 + (j & 4) * 1024;
@@ -712,10 +724,15 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
       for (int j = 0; j < TJ; ++j) xa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, 0, 0);
     }
+    // the weight row of W tile row wbase + wtile(i) + (ln & 31) (kg_wrow): for the fused mode the gate or up
+    // half is known per i, so the row is a sum of uniform terms and the lane's row, with no per-lane select
+    // (which would keep a vector copy of `half` live across the loop)
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
-      xb[i] = __builtin_amdgcn_raw_buffer_load_b32(
-          rsb, (unsigned)(kg_wrow<MODE, 256>(n0, half, wbase + wtile(i) + (ln & 31)) * 4 + kg4 * p.n * 4), 0, 0);
+    for (int i = 0; i < TI; ++i) {
+      const int wr = FUSED ? (i < TI / 2 ? n0 : half + n0) + wbase + (i % (TI / 2)) * 32 + (ln & 31)
+                           : n0 + wbase + wtile(i) + (ln & 31);
+      xb[i] = __builtin_amdgcn_raw_buffer_load_b32(rsb, (unsigned)(wr * 4 + kg4 * p.n * 4), 0, 0);
+    }
   };
 
   v16f acc[TI][TJ];
@@ -731,21 +748,23 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     asm volatile("" ::: "memory");                                                                        \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
   } while (0)
-  // DMA schedule: in mode 2 instructions 0..3 of stage s + 2 go out right after stage s's barrier and
-  // 4..15 during stage s + 1 (its epilogue stages in the weight rows of the last stage's buffer, which must
-  // stay untouched until the next tile's first stage); in modes 0/1 all 16 go out after the barrier, so a
-  // tile's epilogue stores follow the whole DMA of the next tile's stage 1 (its staging is its own LDS).
+  // DMA schedule: instructions 0..3 of stage s + 2 go out right after stage s's barrier and 4..15 during
+  // stage s + 1, also across tiles: a tile's epilogue runs with only the next tile's first 4 instructions of
+  // its stage 1 (issued from the last stage) in flight, and its stage 1's other 12 go out during its stage
+  // 0.  (The mode 2 epilogue stages its codes in the weight rows of the last stage's buffer, which thus stay
+  // untouched until the next tile's first stage.  The compiler makes an epilogue's first LDS write wait for
+  // all DMA in flight, as it cannot tell the DMA's LDS destination from the epilogue's.)
   constexpr int NPRE = 4;
   // A stage's barrier: this wave's DMA of stage s + 1 has landed (everything but, on PH 2, the 8 scale words
-  // issued after it), and every wave is done with this stage's buffer.  The first PH 0 after a modes 0/1
-  // epilogue leaves its 32 stores per wave in flight (vmcnt 32: they are the newest).
-#define KG_STAGE_BARRIER(PH, FIRST)                                                                        \
+  // issued after it: loads complete in issue order), and every wave is done with this stage's buffer.  A
+  // count that leaves stores in flight would not do: vmcnt covers loads and stores, which may complete out
+  // of order with respect to each other, so with both outstanding only vmcnt(0) shows that a given load
+  // has landed.  A tile's first barrier in modes 0/1 thus also waits for the previous epilogue's stores,
+  // which have had that stage's MFMAs to drain.
+#define KG_STAGE_BARRIER(PH)                                                                               \
   do {                                                                                                    \
     if constexpr ((PH) == 2) {                                                                             \
       asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");                            \
-    } else if constexpr ((FIRST) && !FUSED) {                                                           \
-      if (stores_pending) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");       \
-      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                       \
     } else {                                                                                              \
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                            \
     }                                                                                                     \
@@ -768,7 +787,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
                                                                       (PH), (int)wb[0][o], (PH),          \
                                                                       (int)wa[0][n]);                     \
-          if (t_ < 16 - NPRE && !((FIRST) && !FUSED)) dma1(OTH, D1, K1, NPRE + t_);                     \
+          if (t_ < 16 - NPRE) dma1(OTH, D1, K1, NPRE + t_);                                               \
           if (t_ == 12 && (PH) == 2) {                                                                     \
             KG_ISSUE_ORDER();                                                                             \
             words(wt, wkg, wa[1], wb[1]);                                                                 \
@@ -777,7 +796,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (kh == 0 && t_ >= 1 && t_ <= 4) res[1][t_ - 1] = KG_PFRAG_A(CUR, 1, t_ - 1);                  \
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
-          if (t_ == 25) KG_STAGE_BARRIER(PH, FIRST);                                                       \
+          if (t_ == 25) KG_STAGE_BARRIER(PH);                                                              \
           if (GATHER && (FIRST) && t_ == 25) rowt[nxt.tb][tid] = rown;                                     \
           if (t_ >= 26) {                                                                                 \
             _Pragma("unroll") for (int q_ = 0; q_ < 16; ++q_)                                              \
@@ -809,7 +828,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
                                                                       (PH), (int)wb[0][o], (PH),          \
                                                                       (int)wa[0][n]);                     \
-          if (2 * t_ < 16 - NPRE && !((FIRST) && !FUSED)) {                                            \
+          if (2 * t_ < 16 - NPRE) {                                                                       \
             dma1(OTH, D1, K1, NPRE + 2 * t_);                                                             \
             dma1(OTH, D1, K1, NPRE + 1 + 2 * t_);                                                         \
           }                                                                                               \
@@ -821,7 +840,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (kh == 0 && t_ >= 1 && t_ <= 2) res[1][t_ - 1] = KG_PFRAG_AH(CUR, 1, t_ - 1);                 \
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
-          if (t_ == 13) KG_STAGE_BARRIER(PH, FIRST);                                                       \
+          if (t_ == 13) KG_STAGE_BARRIER(PH);                                                              \
           if (GATHER && (FIRST) && t_ == 13) rowt[nxt.tb][tid] = rown;                                     \
           if (t_ >= 14) {                                                                                 \
             _Pragma("unroll") for (int q_ = 0; q_ < NPRE / 2; ++q_)                                        \
@@ -859,11 +878,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
   for (int q = 0; q < 16; ++q) dma1(st0, dsc, 0, q);
 #pragma unroll
-  for (int q = 0; q < (FUSED ? NPRE : 16); ++q) dma1(st1, dsc, 128, q);
+  for (int q = 0; q < NPRE; ++q) dma1(st1, dsc, 128, q);
   KG_ISSUE_ORDER();
-  if constexpr (FUSED) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  bool stores_pending = false;                  // modes 0/1: the previous tile's epilogue stores in flight
+  asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
 
   for (;;) {
     // mode 3: the next tile's row table entry, loaded now and written after this tile's first barrier (which
@@ -887,14 +904,16 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     // Per group of four stages: blocks of the word group at or past K (K % 512 != 0) get the unit
-    // exponent 127; the DMA of the next group's stages 0, 1 (issued from stages 2, 3) comes from the next
-    // tile in the last group (dsn, K 0), as do the words loaded on PH 2.
+    // exponent 127 (branch-free: a branch on the first group's test, which does not change from tile to
+    // tile, becomes a flag held across the tile loop); the DMA of the next group's stages 0, 1 (issued from
+    // stages 2, 3) comes from the next tile in the last group (dsn, K 0), as do the words loaded on PH 2.
 #define KG_GROUP_START()                                                                                   \
   const int live_b = KB - ks;                                                                              \
-  if (live_b < 4) {                                                                                        \
-    const u32 keep = live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));                               \
-    _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | (0x7f7f7f7fu & ~keep);   \
-    _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | (0x7f7f7f7fu & ~keep);   \
+  {                                                                                                        \
+    const u32 keep = live_b >= 4 ? 0xffffffffu : live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));   \
+    const u32 unit = 0x7f7f7f7fu & ~keep;                                                                  \
+    _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | unit;                    \
+    _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | unit;                    \
   }                                                                                                        \
   const bool lastg = ks + 4 >= KS;                                                                         \
   const KgPTile wt = lastg ? nxt : cur;                                                                    \
@@ -905,7 +924,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
   _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i]
     if (halft) {
-      {                                          // the first group: its stage 0 follows an epilogue
+      {                                          // the first group (mode 3: the next row table at its barrier)
         const int ks = 0;
         KG_GROUP_START();
         KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
@@ -923,7 +942,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
         KG_GROUP_END();
       }
     } else {
-      {                                          // the first group: its stage 0 follows an epilogue
+      {                                          // the first group (mode 3: the next row table at its barrier)
         const int ks = 0;
         KG_GROUP_START();
         KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
@@ -947,14 +966,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
       // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
       kg_fp8_epilogue_silu(p, acc, st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
     } else {
-      // the rest of the next tile's stage 1 goes out before the stores, which then stay in flight across
-      // that tile's first barrier (its first stage issues none of it)
-      KG_ISSUE_ORDER();
-#pragma unroll
-      for (int q = NPRE; q < 16; ++q) dma1(st1, dnx, 128, q);
-      KG_ISSUE_ORDER();
+      // the stores drain during the next tile's first stage (its barrier waits for them)
       kg_fp8_epilogue_lds(p, acc, stg + wave * 4096, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
-      stores_pending = true;
     }
     if (nidx < 0) break;
     ++round;
