@@ -442,7 +442,9 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
           o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
           *reinterpret_cast<uint2*>(wrow + ((c ^ (mr & 7)) << 4)) = o;
         }
-      __builtin_amdgcn_s_waitcnt(0xc07f);         // lgkmcnt(0): this wave's writes are in LDS
+      // no wait between a round's writes and its reads, nor before the next round's writes: one wave's LDS
+      // operations execute in issue order, so its reads see its own earlier writes and its writes do not
+      // overtake its reads (the compiler waits for the read data before each store)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
@@ -454,7 +456,6 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
         __attribute__((ext_vector_type(4))) unsigned d4 = {v.x, v.y, v.z, v.w};
         __builtin_amdgcn_raw_buffer_store_b128(d4, rc, off, 0, 2 /* nt */);
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);         // reads done before the next round's writes
     }
   }
 }
