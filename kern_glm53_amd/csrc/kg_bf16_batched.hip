@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
         *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
       }
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);            // lgkmcnt(0): this wave's staging is in LDS
+  // no wait before the reads: one wave's LDS operations execute in issue order, so they see its own writes
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
@@ -368,7 +368,7 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
           *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
         }
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
+    // (a wave's LDS operations execute in issue order: its reads see its own writes without a wait)
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
