@@ -7,7 +7,8 @@ normed row to the block's output h, with the gate_up GEMM and `silu_moe` fused i
     gather  the routed rows of xq / xsf into mq / msf                   (kg_moe_gather)
     fc1     m-grouped gate_up with the SiLU-mul-quant epilogue -> mq2   (kg_fp8_gemm_psum_silu_quant)
     fc2     m-grouped down -> f2                                        (kg_fp8_gemm_psum)
-    shared  gate_up, silu_mul_quant, down on xq -> sh                    (kg_fp8_gemm, kg_silu_mul_quant)
+    shared  gate_up with the SiLU-mul-quant epilogue (one group: rows   (kg_fp8_gemm_psum_silu_quant,
+            [0, T)), down on xq -> sh                                    kg_fp8_gemm)
     combine h = bf16(sh + sum_k wts f2)                                 (kg_moe_combine)
 
 Buffers follow the reference's sizes (scripts/gen.py:86-87, 285-300): mcap = 8 T + 256 * 128 routed-row slots,
@@ -64,7 +65,7 @@ class MoEBuffers:
         self.mq, self.msf = u8(self.mcap, H), u8(sf_bytes(H, self.mcap))
         self.mq2, self.msf2 = u8(self.mcap, INTER), u8(sf_bytes(INTER, self.mcap))
         self.f2 = torch.empty(self.mcap, H, dtype=torch.bfloat16, device=device)
-        self.sg = torch.empty(x_rows, 2 * INTER, dtype=torch.bfloat16, device=device)
+        self.spsum = i32(1)                       # the shared expert as one group owning rows [0, T)
         self.sq, self.ssf = u8(x_rows, INTER), u8(sf_bytes(INTER, x_rows))
         self.sh = torch.empty(x_rows, H, dtype=torch.bfloat16, device=device)
 
@@ -92,11 +93,13 @@ def moe_block(xn, xq, xsf, w: MoEWeights, b: MoEBuffers, h, T: int | None = None
     ops.fp8_gemm_psum(b.mq2, w.w2, b.msf2, w.sf2, b.f2, b.psum, n=H, k=INTER, rows=b.mcap, lda=INTER, ldc=H,
                       sfa_rows=b.mcap)
     mark("fc2")
-    ops.fp8_gemm(xq, w.w_sgu, xsf, w.sf_sgu, b.sg, T, n=2 * INTER, k=H, rows=b.x_rows, lda=H, ldc=2 * INTER,
-                 sfa_rows=b.x_rows)
-    mark("shared_gu")
-    ops.silu_mul_quant(b.sg, INTER, b.sq, b.ssf, b.x_rows, None, T)
-    mark("shared_silu")
+    # the shared expert's gate_up (the reference's dense fp8 GEMM into bf16, then silu_mul_quant) as the
+    # grouped GEMM with the fused epilogue over one group of T rows: the same codes and scale words (the fused
+    # epilogue equals the unfused pair bit for bit), without the [T][4096] bf16 round trip
+    b.spsum.fill_(T)
+    ops.fp8_gemm_psum_silu_quant(xq, w.w_sgu, xsf, w.sf_sgu, b.spsum, b.sq, b.ssf, n=2 * INTER, k=H, rows=b.x_rows,
+                                 lda=H, sfa_rows=b.x_rows, sf_rows=b.x_rows, groups=1)
+    mark("shared_gu_silu_quant")
     ops.fp8_gemm(b.sq, w.w_sdn, b.ssf, w.sf_sdn, b.sh, T, n=H, k=INTER, rows=b.x_rows, lda=INTER, ldc=H,
                  sfa_rows=b.x_rows)
     mark("shared_dn")
