@@ -232,7 +232,7 @@ def moe_block_measure(data, dev, stream, iters=3):
     """The whole MoE block (kern_glm53_amd.moe, scripts/gen.py:435-448) at T = 16384: the router GEMM on the bench's
     activation, routing shaped Zipf-like by the router's score-correction bias (-0.25 ln(1 + rank) over a random
     expert ranking), the bench's expert weights, a synthetic shared expert.  Returns the mean wall time of the
-    block and of each step (HIP events on the launch stream)."""
+    block and of each step (HIP events on the launch stream) over `iters` blocks run back to back."""
     from kern_glm53_amd import moe, ops, synth
 
     g = synth.generator(902, "cuda")
@@ -262,14 +262,20 @@ def moe_block_measure(data, dev, stream, iters=3):
         e.record(stream)
         ends.append((step, e))
 
-    for _ in range(iters):
+    # the blocks are enqueued back to back, with no synchronization between them, and the first is not
+    # counted: a block timed right after a synchronization would charge the host's launch of its first kernel
+    # to the router step
+    marks = []
+    for it in range(iters + 1):
         start = torch.cuda.Event(enable_timing=True)
         start.record(stream)
         ends.clear()
         moe.moe_block(xn, xq, xsf, W, B, out, after=after)
-        torch.cuda.synchronize()
+        marks.append((start, list(ends)))
+    torch.cuda.synchronize()
+    for start, evs in marks[1:]:
         prev = start
-        for step, e in ends:
+        for step, e in evs:
             steps[step] = steps.get(step, 0.0) + prev.elapsed_time(e) / iters
             prev = e
     counts = B.counts[:EXPERTS].cpu()
