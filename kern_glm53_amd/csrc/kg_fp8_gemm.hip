@@ -648,8 +648,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   auto dsrc = [&](const KgPTile& t) { return kg_dma_src(p, t, CN); };
   // DMA instruction q of a stage (0..7: A rows 8 (8 wave + q) .., 8..15: the same W rows) at K offset ko
   // into buffer st; past K, or with no tile, it reads zeros.  A half tile's rows 128.. are read as zeros
-  // (never used).  Instructions 0..3 go out after the barrier of the stage before, 4..15 during the stage
-  // after it: the weight rows of a buffer stay untouched until the next stage begins.
+  // (never used).  Instructions 0..7 (the A rows) go out after the barrier of the stage before, 8..15
+  // during the stage after it: the weight rows of a buffer stay untouched until the next stage begins.
   // The per-instruction row and LDS offsets are formed at each instruction from laundered per-wave bases:
   // kept as 16 precomputed values per buffer, they would not fit in registers (spills, whose reloads wait
   // for the whole DMA queue).
@@ -749,13 +749,15 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     asm volatile("" ::: "memory");                                                                        \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
   } while (0)
-  // DMA schedule: instructions 0..3 of stage s + 2 go out right after stage s's barrier and 4..15 during
-  // stage s + 1, also across tiles: a tile's epilogue runs with only the next tile's first 4 instructions of
-  // its stage 1 (issued from the last stage) in flight, and its stage 1's other 12 go out during its stage
-  // 0.  (The mode 2 epilogue stages its codes in the weight rows of the last stage's buffer, which thus stay
-  // untouched until the next tile's first stage.  The compiler makes an epilogue's first LDS write wait for
-  // all DMA in flight, as it cannot tell the DMA's LDS destination from the epilogue's.)
-  constexpr int NPRE = 4;
+  // DMA schedule: instructions 0..7 (the A rows) of stage s + 2 go out right after stage s's barrier and
+  // 8..15 (the W rows) during stage s + 1, also across tiles: a tile's epilogue runs with the next tile's
+  // stage 1 A rows (issued from the last stage) in flight, and that stage's W rows go out during the next
+  // tile's stage 0.  Against 4 + 12 this split ran every bench GEMM 0.4-2.2% faster; 12 + 4 and 16 + 0 in
+  // modes 0/1 ran 3-10% slower.  (The mode 2 epilogue stages its codes in the weight rows of the last
+  // stage's buffer, which thus stay untouched until the next tile's first stage.  The compiler makes an
+  // epilogue's first LDS write wait for all DMA in flight, as it cannot tell the DMA's LDS destination from
+  // the epilogue's.)
+  constexpr int NPRE = 8;
   // A stage's barrier: this wave's DMA of stage s + 1 has landed (everything but, on PH 2, the 8 scale words
   // issued after it: loads complete in issue order), and every wave is done with this stage's buffer.  A
   // count that leaves stores in flight would not do: vmcnt covers loads and stores, which may complete out
@@ -771,12 +773,12 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     }                                                                                                     \
   } while (0)
   // One stage s (PH = its index in the group of four = the byte of the scale words): 2 K halves x 16
-  // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  Slots 0..11 issue DMA
-  // instructions 4..15 of stage s + 1 into OTH (D1 / K1), one per MFMA; slots 1..4 read the second K
+  // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  Slots 0..7 issue DMA
+  // instructions 8..15 of stage s + 1 into OTH (D1 / K1), one per MFMA; slots 1..4 read the second K
   // half's A fragments; the W fragment of row o + 1 is read at (o, n = 0), the second half's row 0 at
   // slot 12, so the last read of CUR is at slot 24.  The barrier after slot 25 waits for this wave's DMA
   // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 12 after it),
-  // publishes it and frees CUR: slots 26..29 issue instructions 0..3 of stage s + 2 into CUR (D2 / K2),
+  // publishes it and frees CUR: slots 26..31 issue instructions 0..7 of stage s + 2 into CUR (D2 / K2),
   // slots 26..30 read stage s + 1's first fragments from OTH.
 #define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                     \
   do {                                                                                                    \
@@ -816,8 +818,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 
   // Half tiles (at most 128 rows, an expert's tail): the 4 waves split 2 x 2 over 128 x 256, so a wave
   // owns rows wm * 64 + 32 j (j < 2) against the same 128 weight rows: 2 x 8 MFMAs per stage, slot
-  // t = 8 kh + 2 o + n.  The same 16 DMA instructions per stage, two per slot: 4..15 of stage s + 1 in
-  // slots 0..5, 0..3 of stage s + 2 in slots 14, 15; the last read of CUR is at slot 12, the barrier
+  // t = 8 kh + 2 o + n.  The same 16 DMA instructions per stage: 8..15 of stage s + 1 in slots 0..3 (two
+  // per slot), 0..7 of stage s + 2 in slots 14, 15 (four per slot); the last read of CUR is at slot 12, the barrier
   // after slot 13; the words go out at slot 6 of PH 2.
 #define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                    \
   do {                                                                                                    \
@@ -871,7 +873,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     __syncthreads();
   }
 
-  // ---- prologue: the first word group, stage 0 and instructions 0..3 of stage 1 (as the ring has them
+  // ---- prologue: the first word group, stage 0 and instructions 0..7 of stage 1 (as the ring has them
   // at a stage's start)
   KgDmaSrc dsc = dsrc(cur), dnx = dsrc(nxt);     // this tile's and the next tile's DMA sources
   words(cur, 0, wa[0], wb[0]);
@@ -881,7 +883,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #pragma unroll
   for (int q = 0; q < NPRE; ++q) dma1(st1, dsc, 128, q);
   KG_ISSUE_ORDER();
-  asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 
   for (;;) {
     // mode 3: the next tile's row table entry, loaded now and written after this tile's first barrier (which
