@@ -773,11 +773,12 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     }                                                                                                     \
   } while (0)
   // One stage s (PH = its index in the group of four = the byte of the scale words): 2 K halves x 16
-  // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  Slots 0..7 issue DMA
-  // instructions 8..15 of stage s + 1 into OTH (D1 / K1), one per MFMA; slots 1..4 read the second K
+  // MFMAs from buffer CUR (stage s + 1 is in OTH).  Slot t = 16 kh + 4 o + n.  The even slots 0..14 issue
+  // DMA instructions 8..15 of stage s + 1 into OTH (D1 / K1), one every other MFMA (one per MFMA in slots
+  // 0..7, or from slot 4 on, ran 0.5% slower at the bench shapes); slots 1..4 read the second K
   // half's A fragments; the W fragment of row o + 1 is read at (o, n = 0), the second half's row 0 at
   // slot 12, so the last read of CUR is at slot 24.  The barrier after slot 25 waits for this wave's DMA
-  // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 12 after it),
+  // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 16 after it),
   // publishes it and frees CUR: slots 26..31 issue instructions 0..7 of stage s + 2 into CUR (D2 / K2),
   // slots 26..30 read stage s + 1's first fragments from OTH.
 #define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                     \
@@ -790,8 +791,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           acc[o][n] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(str[o & 1], res[kh][n], acc[o][n], 0, 0, \
                                                                       (PH), (int)wb[0][o], (PH),          \
                                                                       (int)wa[0][n]);                     \
-          if (t_ < 16 - NPRE) dma1(OTH, D1, K1, NPRE + t_);                                               \
-          if (t_ == 12 && (PH) == 2) {                                                                     \
+          if (t_ % 2 == 0 && t_ < 2 * (16 - NPRE)) dma1(OTH, D1, K1, NPRE + t_ / 2);                      \
+          if (t_ == 16 && (PH) == 2) {                                                                     \
             KG_ISSUE_ORDER();                                                                             \
             words(wt, wkg, wa[1], wb[1]);                                                                 \
             KG_ISSUE_ORDER();                                                                             \
