@@ -186,10 +186,12 @@ int kg_kv_dequant(const void* kv, const int* block_table, int max_pages, const i
 /* FlashInfer routingPrecomputed tables (the `routing(experts, topk, tile)` op, scripts/glm_ops.py:207-233;
  * three launches as there).  ids int32 [T][topk] -> counts [2*experts] (upper half zero), cta_batch /
  * cta_limit [ctas], num_non_exiting [1], total_padded [1], route_map [mcap], exp2perm [T][topk];
- * expert e's rows start at 2^tile_log2 times its CTA offset and, within an expert, follow ascending
- * expanded index.  Requires experts <= 256 (the reference's op has 256), topk <= 16, T * topk <= 4194304,
- * route_map of at least topk*T + experts*2^tile_log2 entries and cta_batch / cta_limit of at least
- * ceil(topk*T / 2^tile_log2) + experts (the reference's mcap = 8T + 256*128 and mcap/128, gen.py:86-87).
+ * expert e's rows start at 128 times its CTA offset and, within an expert, follow ascending expanded index.
+ * Requires tile_log2 == 7 (the reference's op fixes the tile at 128 rows, scripts/gen.py:146; its buffers are
+ * sized for it, and a larger tile could write past route_map), experts <= 256 (the reference's op has 256),
+ * topk <= 16, T * topk <= 4194304, route_map of at least topk*T + experts*128 entries and cta_batch /
+ * cta_limit of at least ceil(topk*T / 128) + experts (the reference's mcap = 8T + 256*128 and mcap/128,
+ * gen.py:86-87).
  * The segment table is a 1 MiB static device array of the library: calls on one device must be
  * stream-ordered. */
 int kg_moe_routing(const int* ids, int T, int topk, int experts, int tile_log2, int* counts, int* cta_batch,

@@ -468,8 +468,8 @@ KG_DEV void kg_fp8_epilogue_lds(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
 // pair with its up accumulators i + 2 at the same output columns.  Same arithmetic as the unfused pair
 // (bf16 gate_up output, then glm_silu_mul_quant): g and u are rounded to bf16, v = bf16(silu(g) u), the
 // 128-column amax goes through LDS (xam) to the wave holding the other 64 columns of the row.  The e4m3
-// codes of the whole 256 x 128 output tile are staged in LDS (the weight half of the last stage's
-// buffer, which no DMA writes before the next tile's first stage: row r at r * 128 with 16-byte chunk c
+// codes of the whole 256 x 128 output tile are staged in LDS (a 32 KB half of the last stage's buffer,
+// which no DMA writes before the next tile's first stage: row r at r * 128 with 16-byte chunk c
 // in slot c ^ (r & 7)) and then stored a full 128-byte row segment per 8 lanes: every wave issues 8 code
 // stores and 1 exponent-byte store (offsets past the resource drop the rows past the tile).
 KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage, float (*xam)[256], u8* xe,
@@ -660,7 +660,10 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   const unsigned wrow_w = (unsigned)kg_wrow<MODE, 256>(0, half, wave * 64) * (unsigned)p.k;
   // A load with nothing to fetch (K padding, no tile, a half tile's A rows 128..) gets a row base past the
   // resource (KG_OOB: the VGPR offset stays below 2^32, as 64 lda and 64 k are below 2^31), so it reads zeros.
-  auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int q) {
+  auto dma1 = [&](u8* st, const KgDmaSrc& d, int ko, int qi) {
+    // mode 2: the weight rows (the HBM stream) go right after a stage's barrier and the A rows during the next
+    // stage (gate_up 0.7% faster; the down GEMM ran 2% slower so, and modes 0/1 keep A first)
+    const int q = MODE == 2 ? qi ^ 8 : qi;
     const int j = q & 7;
     unsigned v;
     if (GATHER && q < 8) {
@@ -756,10 +759,11 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // 8..15 (the W rows) during stage s + 1, also across tiles: a tile's epilogue runs with the next tile's
   // stage 1 A rows (issued from the last stage) in flight, and that stage's W rows go out during the next
   // tile's stage 0.  Against 4 + 12 this split ran every bench GEMM 0.4-2.2% faster; 12 + 4 and 16 + 0 in
-  // modes 0/1 ran 3-10% slower.  (The mode 2 epilogue stages its codes in the weight rows of the last
-  // stage's buffer, which thus stay untouched until the next tile's first stage.  The compiler makes an
-  // epilogue's first LDS write wait for all DMA in flight, as it cannot tell the DMA's LDS destination from
-  // the epilogue's.)
+  // modes 0/1 ran 3-10% slower.  Mode 2 swaps the two halves (the weight rows, its HBM stream, right after
+  // the barrier: gate_up 0.7% faster; the same swap ran the down GEMM 2% slower).  (The fused epilogue stages
+  // its codes in the half of the last stage's buffer that the ring refills only during the next tile's first
+  // stage: the A rows in mode 2, the weight rows in mode 3.  The compiler makes an epilogue's first LDS write
+  // wait for all DMA in flight, as it cannot tell the DMA's LDS destination from the epilogue's.)
   constexpr int NPRE = 8;
   // A stage's barrier: this wave's DMA of stage s + 1 has landed (everything but, on PH 2, the 8 scale words
   // issued after it: loads complete in issue order), and every wave is done with this stage's buffer.  A
@@ -970,8 +974,10 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 #undef KG_GROUP_START
 #undef KG_GROUP_END
     if constexpr (FUSED) {
-      // the weight rows of buffer 1 (the last stage's) are not written before the next tile's stage 0
-      kg_fp8_epilogue_silu(p, acc, st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
+      // mode 2 stages in the A rows of the last stage's buffer (it issues the weight rows after a barrier
+      // and the A rows during the next stage), mode 3 in its weight rows (the other order)
+      kg_fp8_epilogue_silu(p, acc, MODE == 2 ? st1 : st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn,
+                           halft);
     } else {
       // the stores drain during the next tile's first stage (its barrier waits for them)
       kg_fp8_epilogue_lds(p, acc, stg + wave * 4096, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);

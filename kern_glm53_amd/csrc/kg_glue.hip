@@ -216,11 +216,11 @@ extern "C" int kg_moe_routing(const int* ids, int T, int topk, int experts, int 
                               int* cta_batch, int* cta_limit, int* num_non_exiting, int* total_padded,
                               int* route_map, int* exp2perm, void* stream) {
   KG_CHECK(ids && counts && cta_batch && cta_limit && num_non_exiting && total_padded && route_map && exp2perm);
-  // experts <= 256 keeps the padded rows (at most topk * T + experts * (2^tile_log2 - 1)) and the row blocks
-  // within the reference's buffers, route_map [topk * T + 256 * 128] and cta_* [that / 128]
-  // (scripts/gen.py:86-87, 289-293), at its tile of 128
-  KG_CHECK(T >= 0 && topk >= 1 && topk <= 16 && experts >= 1 && experts <= KG_MAX_EXPERTS && tile_log2 >= 0 &&
-           tile_log2 <= 10);
+  // The reference's op fixes the tile at 128 rows (mPaddingLog2 = 7, scripts/gen.py:146), and its buffers are
+  // sized for it: route_map [topk * T + 256 * 128] and cta_* [that / 128] (scripts/gen.py:86-87, 289-293).
+  // experts <= 256 keeps the padded rows (at most topk * T + experts * 127) and the row blocks inside them; a
+  // larger tile could write past route_map, so any other tile is rejected.
+  KG_CHECK(T >= 0 && topk >= 1 && topk <= 16 && experts >= 1 && experts <= KG_MAX_EXPERTS && tile_log2 == 7);
   const long long total = (long long)T * topk;
   KG_CHECK(total <= (long long)KG_SEG * KG_MAX_SEGS);
   const int nseg = (int)((total + KG_SEG - 1) / KG_SEG);

@@ -377,37 +377,75 @@ extern "C" int kg_topk_slots(int* ind, const int* block_table, int max_pages, co
 
 // ============================================================================ cache gathers
 
-// Block b of a launch -> (sequence s, its page j, the stream row of the page's first row), as the reference
-// walks the sequences (source/glm_glue.cu:360-367); false past the last page.
-KG_DEV bool kg_page_of(int b, const int* seq_lens, int nseq, int& s, int& j, unsigned& row0, int& n) {
-  unsigned goff = 0;
-  for (s = 0; s < nseq; ++s) {
-    const int len = seq_lens[s], pages = (len + KG_PAGE - 1) / KG_PAGE;
-    if (b < pages) {
-      j = b;
-      row0 = goff + (unsigned)(b * KG_PAGE);
-      n = min(KG_PAGE, len - b * KG_PAGE);
+// Both gathers lay each sequence's paged cache rows out back to back: page j of sequence s (its rows
+// [64 j, min(64 j + 64, len))) lands at stream rows goff(s) + 64 j, goff(s) = the tokens of the sequences
+// before s (source/glm_glue.cu:353-414).  The launch's pages are numbered across the sequences in order;
+// every wave of a workgroup takes its own page.
+
+constexpr int KG_GATHER_WAVES = 4;                 // pages (waves) per workgroup
+
+KG_DEV __amdgpu_buffer_rsrc_t kg_rsrc_g(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Flat page b -> (sequence s, its page j, the stream row row0 of the page's first row, its live rows n), or
+// false past the last page.  The wave scans 64 sequences at a time: lane l holds sequence s0 + l's token
+// count and page count, a wave-wide inclusive prefix sum of both gives the pages and tokens up to it, and a
+// ballot picks the first sequence whose pages reach past b.
+KG_DEV bool kg_wave_page(int b, const int* __restrict__ seq_lens, int nseq, int& s, int& j, unsigned& row0, int& n) {
+  const int lane = (int)threadIdx.x & 63;
+  int pbase = 0;
+  unsigned tbase = 0;
+  for (int s0 = 0; s0 < nseq; s0 += 64) {
+    const int len = s0 + lane < nseq ? seq_lens[s0 + lane] : 0;
+    const int pg = (len + KG_PAGE - 1) / KG_PAGE;
+    int ip = pg;
+    unsigned it = (unsigned)len;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int vp = __shfl_up(ip, o, 64);
+      const unsigned vt = __shfl_up(it, o, 64);
+      if (lane >= o) ip += vp, it += vt;
+    }
+    const unsigned long long hit = __ballot(pbase + ip > b);
+    if (hit) {
+      const int L = __ffsll((long long)hit) - 1;
+      const int ipl = __shfl(ip, L, 64), pgl = __shfl(pg, L, 64), lenl = __shfl(len, L, 64);
+      const unsigned itl = __shfl(it, L, 64);
+      s = s0 + L;
+      j = b - (pbase + ipl - pgl);
+      row0 = tbase + (itl - (unsigned)lenl) + (unsigned)(j * KG_PAGE);
+      n = min(KG_PAGE, lenl - j * KG_PAGE);
       return true;
     }
-    b -= pages;
-    goff += (unsigned)len;
+    pbase += __shfl(ip, 63, 64);
+    tbase += __shfl(it, 63, 64);
   }
   return false;
 }
 
-// glm_idx_gather (source/glm_glue.cu:353-376): a workgroup per page, 16 bytes per thread, the scales by
-// the first n threads.
-__global__ __launch_bounds__(256) void kg_idx_gather_kernel(const u8* __restrict__ idx, const int* __restrict__ block_table,
-                                                            int max_pages, const int* __restrict__ seq_lens, int nseq,
-                                                            u8* __restrict__ kg, float* __restrict__ ksf) {
+// glm_idx_gather (source/glm_glue.cu:353-376).  A cache page is 64 rows of 128 e4m3 codes, then 64 f32 scales.
+// The wave moves its page's codes as 8 loads of 1 KB (8 rows each, lane l the 16-byte piece l of them), all in
+// flight before the 8 stores, and lane r the scale of row r.  The source and destination resources end at the
+// page's live rows: pieces past them read zeros and their stores drop.
+__global__ __launch_bounds__(64 * KG_GATHER_WAVES) void kg_idx_gather_kernel(
+    const u8* __restrict__ idx, const int* __restrict__ block_table, int max_pages, const int* __restrict__ seq_lens,
+    int nseq, u8* __restrict__ kg, float* __restrict__ ksf, int blocks) {
+  const int page = (int)blockIdx.x * KG_GATHER_WAVES + (int)(threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
   int s, j, n;
   unsigned row0;
-  if (!kg_page_of((int)blockIdx.x, seq_lens, nseq, s, j, row0, n)) return;
+  if (page >= blocks || !kg_wave_page(page, seq_lens, nseq, s, j, row0, n)) return;
   const u8* src = idx + (size_t)block_table[(size_t)s * max_pages + j] * KG_IDX_PAGE;
-  const uint4* sv = reinterpret_cast<const uint4*>(src);
-  uint4* dv = reinterpret_cast<uint4*>(kg + (size_t)row0 * KG_ID);
-  for (int i = threadIdx.x; i < n * (KG_ID / 16); i += 256) dv[i] = sv[i];
-  if ((int)threadIdx.x < n) ksf[row0 + threadIdx.x] = reinterpret_cast<const float*>(src + KG_PAGE * KG_ID)[threadIdx.x];
+  const __amdgpu_buffer_rsrc_t rs = kg_rsrc_g(src, (unsigned)(n * KG_ID));
+  const __amdgpu_buffer_rsrc_t rd = kg_rsrc_g(kg + (size_t)row0 * KG_ID, (unsigned)(n * KG_ID));
+  __attribute__((ext_vector_type(4))) unsigned v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (unsigned)((i * 64 + lane) * 16), 0, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) __builtin_amdgcn_raw_buffer_store_b128(v[i], rd, (unsigned)((i * 64 + lane) * 16), 0, 0);
+  const unsigned sc = __builtin_amdgcn_raw_buffer_load_b32(kg_rsrc_g(src + KG_PAGE * KG_ID, (unsigned)(n * 4)),
+                                                           (unsigned)(lane * 4), 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(sc, kg_rsrc_g(ksf + row0, (unsigned)(n * 4)), (unsigned)(lane * 4), 0, 0);
 }
 
 extern "C" int kg_idx_gather(const void* idx, const int* block_table, int max_pages, const int* seq_lens, int nseq,
@@ -415,37 +453,54 @@ extern "C" int kg_idx_gather(const void* idx, const int* block_table, int max_pa
   KG_CHECK(idx && block_table && seq_lens && kg && ksf && max_pages > 0 && nseq >= 0 && blocks >= 0);
   KG_CHECK(kg_aligned(idx, 16) && kg_aligned(kg, 16));
   if (blocks == 0) return 0;
-  hipLaunchKernelGGL(kg_idx_gather_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const u8*)idx,
-                     block_table, max_pages, seq_lens, nseq, (u8*)kg, ksf);
+  hipLaunchKernelGGL(kg_idx_gather_kernel, dim3((blocks + KG_GATHER_WAVES - 1) / KG_GATHER_WAVES),
+                     dim3(64 * KG_GATHER_WAVES), 0, (hipStream_t)stream, (const u8*)idx, block_table, max_pages,
+                     seq_lens, nseq, (u8*)kg, ksf, blocks);
   return (int)hipGetLastError();
 }
 
-// glm_kv_dequant (source/glm_glue.cu:378-414): fp8 latent rows -> bf16 [576] rows of the stream, value =
-// bf16(f32(e4m3) * tile scale), k_pe copied.  A workgroup per page, a 32-lane half wave per row: lane l
-// converts 16 codes (tile l >> 3) into 32 bytes, lanes 0-7 copy the 128 bytes of k_pe.
-__global__ __launch_bounds__(256) void kg_kv_dequant_kernel(const u8* __restrict__ kv, const int* __restrict__ block_table,
-                                                            int max_pages, const int* __restrict__ seq_lens, int nseq,
-                                                            u16* __restrict__ kvd) {
+// glm_kv_dequant (source/glm_glue.cu:378-414).  An fp8 latent row is 656 bytes: 512 e4m3 codes, 4 f32 scales
+// (one per 128 codes), 64 bf16 of k_pe; its bf16 row is 576 values, bf16(f32(code) * scale) then k_pe.  The
+// wave takes its page's rows four at a time: lane l converts codes [8 l, 8 l + 8) of a row (an 8-byte load,
+// scale l >> 4, a 16-byte store: each instruction covers the row's 512 bytes / 1 KB contiguously), lanes 0-7
+// move the 128 bytes of k_pe.  Resources end at the page's live rows, so a fourth row past them reads zeros and
+// stores nothing.
+__global__ __launch_bounds__(64 * KG_GATHER_WAVES) void kg_kv_dequant_kernel(
+    const u8* __restrict__ kv, const int* __restrict__ block_table, int max_pages, const int* __restrict__ seq_lens,
+    int nseq, u16* __restrict__ kvd, int blocks) {
+  const int page = (int)blockIdx.x * KG_GATHER_WAVES + (int)(threadIdx.x >> 6), lane = (int)threadIdx.x & 63;
   int s, j, n;
   unsigned row0;
-  if (!kg_page_of((int)blockIdx.x, seq_lens, nseq, s, j, row0, n)) return;
-  const int hw = threadIdx.x >> 5, l = threadIdx.x & 31;
-  const u8* page = kv + (size_t)block_table[(size_t)s * max_pages + j] * KG_PAGE * KG_KV8;
-  for (int i = hw; i < n; i += 8) {
-    const u8* src = page + (size_t)i * KG_KV8;
-    u8* dst = reinterpret_cast<u8*>(kvd + ((size_t)row0 + i) * KG_MLA);
-    const uint4 q = *reinterpret_cast<const uint4*>(src + l * 16);
-    const float sc = reinterpret_cast<const float*>(src + KG_KVL)[l >> 3];
-    const u32 qw[4] = {q.x, q.y, q.z, q.w};
-    u32 o[8];
+  if (page >= blocks || !kg_wave_page(page, seq_lens, nseq, s, j, row0, n)) return;
+  const u8* src = kv + (size_t)block_table[(size_t)s * max_pages + j] * KG_PAGE * KG_KV8;
+  const __amdgpu_buffer_rsrc_t rs = kg_rsrc_g(src, (unsigned)(n * KG_KV8));
+  const __amdgpu_buffer_rsrc_t rd = kg_rsrc_g(kvd + (size_t)row0 * KG_MLA, (unsigned)(n * KG_MLA * 2));
+  const unsigned pe_off = lane < 8 ? (unsigned)(KG_KVL + 16 + lane * 16) : 0x80000000u;   // k_pe lanes
+  for (int i0 = 0; i0 < n; i0 += 4) {
+    __attribute__((ext_vector_type(2))) unsigned c[4];
+    __attribute__((ext_vector_type(4))) unsigned pe[4];
+    unsigned sc[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const u32 b0 = (qw[k >> 1] >> (16 * (k & 1))) & 0xffu, b1 = (qw[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;
-      o[k] = kg_pack_bf16x2(kg_e4m3_to_f32(b0) * sc, kg_e4m3_to_f32(b1) * sc);
+    for (int u = 0; u < 4; ++u) {
+      const unsigned r = (unsigned)((i0 + u) * KG_KV8);
+      c[u] = __builtin_amdgcn_raw_buffer_load_b64(rs, r + (unsigned)(lane * 8), 0, 0);
+      sc[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, r + (unsigned)(KG_KVL + (lane >> 4) * 4), 0, 0);
+      pe[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, r + pe_off, 0, 0);
     }
-    reinterpret_cast<uint4*>(dst + l * 32)[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    reinterpret_cast<uint4*>(dst + l * 32)[1] = make_uint4(o[4], o[5], o[6], o[7]);
-    if (l < 8) reinterpret_cast<uint4*>(dst + KG_KVL * 2)[l] = reinterpret_cast<const uint4*>(src + KG_KVL + 16)[l];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float f = kg_u2f(sc[u]);
+      __attribute__((ext_vector_type(4))) unsigned o;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const u32 wd = c[u][h >> 1] >> (16 * (h & 1));
+        o[h] = kg_pack_bf16x2(kg_e4m3_to_f32(wd & 0xffu) * f, kg_e4m3_to_f32((wd >> 8) & 0xffu) * f);
+      }
+      const unsigned r = (unsigned)((i0 + u) * KG_MLA * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(o, rd, r + (unsigned)(lane * 16), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(pe[u], rd, lane < 8 ? r + (unsigned)(KG_KVL * 2 + lane * 16) : 0x80000000u,
+                                             0, 0);
+    }
   }
 }
 
@@ -454,7 +509,8 @@ extern "C" int kg_kv_dequant(const void* kv, const int* block_table, int max_pag
   KG_CHECK(kv && block_table && seq_lens && kvd && max_pages > 0 && nseq >= 0 && blocks >= 0);
   KG_CHECK(kg_aligned(kv, 16) && kg_aligned(kvd, 16));
   if (blocks == 0) return 0;
-  hipLaunchKernelGGL(kg_kv_dequant_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const u8*)kv,
-                     block_table, max_pages, seq_lens, nseq, (u16*)kvd);
+  hipLaunchKernelGGL(kg_kv_dequant_kernel, dim3((blocks + KG_GATHER_WAVES - 1) / KG_GATHER_WAVES),
+                     dim3(64 * KG_GATHER_WAVES), 0, (hipStream_t)stream, (const u8*)kv, block_table, max_pages,
+                     seq_lens, nseq, (u16*)kvd, blocks);
   return (int)hipGetLastError();
 }

@@ -133,56 +133,68 @@ __global__ __launch_bounds__(512, 2) void kg_mqa_logits_kernel(const u8* __restr
   };
   // Logits of a block's key tiles 0, 1: v_permlane32_swap trades the high half of tile 0's partial sums for
   // the low half of tile 1's, so one add gives lane l < 32 the sum of tile 0's key l and lane l >= 32 that
-  // of tile 1's key l - 32 (the same low + high order on both), i.e. key kb + l.  Then the key scale and
-  // one store of 64 consecutive logits, always issued: a key outside [ks, ke) or past stride gets an
-  // offset past the row, which drops it.
+  // of tile 1's key l - 32 (the same low + high order on both), i.e. key kb + l; then the key scale.  The
+  // store of the 64 consecutive logits is always issued: a key outside [ks, ke) or past stride (or no block
+  // yet) gets an offset past the row, which drops it.
   const unsigned lrel = (unsigned)lane - k0;
   const unsigned lim = live && k1 > k0 ? min(k1 - k0, (unsigned)stride) : 0u;
-  auto store = [&](float x, float y, float sc, unsigned kb) {
+  auto logit = [&](float x, float y, float sc) {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-    const float v = (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * sc;
+    return (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * sc;
+  };
+  auto store = [&](float v, unsigned kb, bool any) {
     const unsigned rel = kb + lrel;
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rlg, rel < lim ? rel * 4u : 0x80000000u, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rlg, any && rel < lim ? rel * 4u : 0x80000000u, 0, 0);
   };
 
   // Software pipeline over key blocks (two stages, two accumulator sets): the MFMAs of block i + 1 issue
   // between the epilogue steps of block i, so the matrix pipe and the VALU overlap.  Per block:
   //   read block i's key scales (its stage);
-  //   barrier: the DMA of block i + 1 has landed (issued before the previous block's logits store; nothing
-  //            is stored before the first block) and every wave is done reading block i's stage;
-  //   DMA of block i + 2 into block i's stage; MFMAs of block i + 1 interleaved with block i's epilogue.
+  //   barrier: vmcnt(0), i.e. the DMA of block i + 1 and the store of block i - 2's logits (both issued right
+  //            after the previous barrier, a block ago) are complete, and every wave is done reading block i's
+  //            stage.  vmcnt counts loads and stores together and the two may complete out of order with
+  //            respect to each other, so with a store in flight only vmcnt(0) shows that a load has landed;
+  //            issuing the store ahead of the DMA gives both a whole block to complete before that wait;
+  //   the store of block i - 1's logits, the DMA of block i + 2 into block i's stage, then the MFMAs of
+  //   block i + 1 interleaved with block i's epilogue, whose logits are stored after the next barrier.
   // The last block's MFMAs of the following stage run on whatever it holds and are discarded.
   v16f acc0[TB], acc1[TB];
   issue(st0, kmin);
   issue(st1, kmin + BK);                         // (past kmax or num_kv: read, never stored)
   asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
-  static_assert(NQ == 1 && TB == 2, "the waits count 2 DMA instructions and 1 store per block");
+  static_assert(NQ == 1 && TB == 2, "the prologue's wait counts 2 DMA instructions per block");
 #pragma unroll
   for (int t = 0; t < TB; ++t) mfma(st0, acc0[t], t);
 
-#define KG_MQA_BLOCK(CUR, NXT, AC, AN, VMCNT)                                                               \
+#define KG_MQA_BLOCK(CUR, NXT, AC, AN)                                                                      \
   do {                                                                                                    \
     const float sc_ = *reinterpret_cast<const float*>((CUR) + KEYB + lane * 4);                           \
-    asm volatile("s_waitcnt vmcnt(" VMCNT ") lgkmcnt(0)\n\ts_barrier" ::: "memory");                      \
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                              \
+    store(vp, kbp, anyp);                                                                                 \
     issue(CUR, kb + 2 * BK);                                                                              \
-    __builtin_amdgcn_sched_barrier(0);             /* the DMA goes out first */                           \
+    __builtin_amdgcn_sched_barrier(0);             /* the store and the DMA go out first */               \
     mfma(NXT, AN[0], 0);                                                                                  \
     const float h0_ = hsum(AC[0]);                                                                        \
     mfma(NXT, AN[1], 1);                                                                                  \
     const float h1_ = hsum(AC[1]);                                                                        \
-    store(h0_, h1_, sc_, kb);                                                                             \
+    vp = logit(h0_, h1_, sc_);                                                                            \
+    kbp = kb;                                                                                             \
+    anyp = true;                                                                                          \
     kb += BK;                                                                                             \
   } while (0)
   // Blocks go in pairs with one exit test per pair, so that each block is one basic block and its MFMAs
   // stay between its epilogue steps; a pair's second block may lie past kmax: its keys are past every
   // row's ke, so its store drops.
-  unsigned kb = kmin;
-  KG_MQA_BLOCK(st0, st1, acc0, acc1, "0");       // the first block: nothing stored yet
+  unsigned kb = kmin, kbp = kmin;
+  float vp = 0.0f;
+  bool anyp = false;                             // no logits computed before the first block
+  KG_MQA_BLOCK(st0, st1, acc0, acc1);
   while (kb < kmax) {
-    KG_MQA_BLOCK(st1, st0, acc1, acc0, "1");
-    KG_MQA_BLOCK(st0, st1, acc0, acc1, "1");
+    KG_MQA_BLOCK(st1, st0, acc1, acc0);
+    KG_MQA_BLOCK(st0, st1, acc0, acc1);
   }
 #undef KG_MQA_BLOCK
+  store(vp, kbp, true);                          // the last block's logits
   __builtin_amdgcn_s_waitcnt(0);                 // no DMA into LDS may be in flight at exit
 }
 

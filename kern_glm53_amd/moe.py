@@ -9,11 +9,13 @@ normed row to the block's output h, with the gate_up GEMM and `silu_moe` fused i
     fc2     m-grouped down -> f2                                        (kg_fp8_gemm_psum)
     shared  gate_up with the SiLU-mul-quant epilogue (one group: rows   (kg_fp8_gemm_psum_silu_quant,
             [0, T)), down on xq -> sh                                    kg_fp8_gemm)
+            (a chunk of x_rows not a multiple of 128: the dense gate_up  (kg_fp8_gemm, kg_silu_mul_quant)
+            GEMM into bf16, then silu_mul_quant, as the reference does)
     combine h = bf16(sh + sum_k wts f2)                                 (kg_moe_combine)
 
 Buffers follow the reference's sizes (scripts/gen.py:86-87, 285-300): mcap = 8 T + 256 * 128 routed-row slots,
 scale words for `x_rows` rows (the chunk).  Every buffer is allocated once by `MoEBuffers`; a call allocates
-nothing.  The routed-row buffers start zeroed: the GEMMs read (and never store) their padding rows.  Weights
+nothing, and with T = MoEBuffers.T (the default) every launch of the block is one of this library's kernels.  The routed-row buffers start zeroed: the GEMMs read (and never store) their padding rows.  Weights
 are the reference's operand layouts (glm_requant's output): w13 [256 * 4096][6144] with scale words
 [256 * 12][4096], w2 [256 * 6144][2048] with [256 * 4][6144], the shared expert's w_sgu [4096][6144] /
 [12][4096] and w_sdn [6144][2048] / [4][6144].
@@ -65,7 +67,13 @@ class MoEBuffers:
         self.mq, self.msf = u8(self.mcap, H), u8(sf_bytes(H, self.mcap))
         self.mq2, self.msf2 = u8(self.mcap, INTER), u8(sf_bytes(INTER, self.mcap))
         self.f2 = torch.empty(self.mcap, H, dtype=torch.bfloat16, device=device)
-        self.spsum = i32(1)                       # the shared expert as one group owning rows [0, T)
+        # the shared expert's gate_up: the fused grouped GEMM over one group owning rows [0, T) (its psum written
+        # here, once) needs x_rows in 128-row blocks (it reads A rows up to x_rows rounded up to 128); other
+        # chunks take the dense GEMM into bf16 and silu_mul_quant
+        self.fused_shared = x_rows % 128 == 0
+        self.spsum = torch.full((1,), T, dtype=torch.int32, device=device)
+        self.spsum_T = T                          # the value spsum holds
+        self.sgu = None if self.fused_shared else torch.empty(x_rows, 2 * INTER, dtype=torch.bfloat16, device=device)
         self.sq, self.ssf = u8(x_rows, INTER), u8(sf_bytes(INTER, x_rows))
         self.sh = torch.empty(x_rows, H, dtype=torch.bfloat16, device=device)
 
@@ -96,9 +104,16 @@ def moe_block(xn, xq, xsf, w: MoEWeights, b: MoEBuffers, h, T: int | None = None
     # the shared expert's gate_up (the reference's dense fp8 GEMM into bf16, then silu_mul_quant) as the
     # grouped GEMM with the fused epilogue over one group of T rows: the same codes and scale words (the fused
     # epilogue equals the unfused pair bit for bit), without the [T][4096] bf16 round trip
-    b.spsum.fill_(T)
-    ops.fp8_gemm_psum_silu_quant(xq, w.w_sgu, xsf, w.sf_sgu, b.spsum, b.sq, b.ssf, n=2 * INTER, k=H, rows=b.x_rows,
-                                 lda=H, sfa_rows=b.x_rows, sf_rows=b.x_rows, groups=1)
+    if b.fused_shared:
+        if T != b.spsum_T:                      # a call of another length than the last one
+            b.spsum.fill_(T)
+            b.spsum_T = T
+        ops.fp8_gemm_psum_silu_quant(xq, w.w_sgu, xsf, w.sf_sgu, b.spsum, b.sq, b.ssf, n=2 * INTER, k=H,
+                                     rows=b.x_rows, lda=H, sfa_rows=b.x_rows, sf_rows=b.x_rows, groups=1)
+    else:
+        ops.fp8_gemm(xq, w.w_sgu, xsf, w.sf_sgu, b.sgu, T, n=2 * INTER, k=H, rows=b.x_rows, lda=H, ldc=2 * INTER,
+                     sfa_rows=b.x_rows)
+        ops.silu_mul_quant(b.sgu, INTER, b.sq, b.ssf, b.x_rows, None, T)
     mark("shared_gu_silu_quant")
     ops.fp8_gemm(b.sq, w.w_sdn, b.ssf, w.sf_sdn, b.sh, T, n=H, k=INTER, rows=b.x_rows, lda=INTER, ldc=H,
                  sfa_rows=b.x_rows)

@@ -166,8 +166,9 @@ def kv_dequant(kv, block_table, max_pages: int, seq_lens, nseq: int, kvd, *, blo
 
 def routing(ids, counts, cta_batch, cta_limit, num_non_exiting, total_padded, route_map, exp2perm, *, T: int,
             experts: int = EXPERTS, topk: int = TOPK, tile: int = TILE):
-    """`routing(experts, topk, tile)` (scripts/glm_ops.py:207-233): FlashInfer routingPrecomputed tables."""
-    assert tile & (tile - 1) == 0, "tile must be a power of two"
+    """`routing(experts, topk, tile)` (scripts/glm_ops.py:207-233): FlashInfer routingPrecomputed tables.  The
+    reference's op fixes tile = 128 (scripts/gen.py:146); the library rejects any other tile (KgError)."""
+    assert tile > 0 and tile & (tile - 1) == 0, "tile must be a power of two"
     call("kg_moe_routing", _ptr(ids), T, topk, experts, tile.bit_length() - 1, _ptr(counts), _ptr(cta_batch),
          _ptr(cta_limit), _ptr(num_non_exiting), _ptr(total_padded), _ptr(route_map), _ptr(exp2perm), _stream())
 

@@ -98,6 +98,9 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     ("kg_moe_routing", [FAKE, 16, 8, 2048, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
     ("kg_moe_routing", [FAKE, 16, 8, 257, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
     ("kg_moe_routing", [FAKE, 16, 32, 256, 7, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
+    # routing: a tile other than the reference's 128 rows (route_map is sized for it; 256 could write past it)
+    ("kg_moe_routing", [FAKE, 16, 8, 256, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
+    ("kg_moe_routing", [FAKE, 16, 8, 256, 6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, NULL]),
     # gather: T > x_rows
     ("kg_moe_gather", [FAKE, FAKE, 8, FAKE, FAKE, FAKE, 1024, 16, NULL]),
     # requant: K % 128, group_rows % 128

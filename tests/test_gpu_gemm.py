@@ -46,10 +46,10 @@ def quant_weight(N, K, seed, groups=1):
     return wq, sfb
 
 
-def check(out_bits, ref32, abs_sum, k, what, model=None):
+def check(out_bits, ref32, abs_sum, k, what, model=None, window=None):
     """The parity bar (module docstring); prints the measured PARITY line."""
     out = torch.from_numpy(out_bits.view(np.int16)).view(torch.bfloat16).float()
-    ok, rep = ref.check_bf16_gemm(out, ref32, abs_sum, k, model32=model)
+    ok, rep = ref.check_bf16_gemm(out, ref32, abs_sum, k, model32=model, window=window)
     line = ref.parity_line(what, rep)
     print(line, flush=True)
     assert ok, line
@@ -97,9 +97,10 @@ def test_fp8_gemm(M, N, K, rows, lda, ldc, sfa_rows):
     rows_m = np.arange(M) if (M, N, K) == (512, 2048, 6144) else sample_rows(M, seed=M + N)
     model = model_on_rows(a, w, sfa, sfb, M, N, K, lda, sfa_rows, rows_m)
     c = filled((rows, ldc), SENTINEL, torch.int16)
+    window = ref.fp8_window_bound(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
     ops.fp8_gemm(d(a), d(w), d(sfa), d(sfb), c, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
     out = h(c, np.uint16)
-    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"dense {M}x{N}x{K}", model)
+    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"dense {M}x{N}x{K}", model, window)
     assert np.all(out[:M, N:] == SENTINEL) and np.all(out[M:] == SENTINEL)
 
 
@@ -130,8 +131,9 @@ def test_fp8_gemm_bench_shapes_sampled(N, K, ldc):
     ref32 = ref.fp8_gemm(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
     S = ref.fp8_gemm_abs(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
     model = ref.fp8_gemm_mfma(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
+    window = ref.fp8_window_bound(a_s, w_h, sfa_s, sfb_h, R, N, K, K, R)
     out = h(c.view(torch.int16), np.uint16)
-    check(np.ascontiguousarray(out[rows, :N]), ref32, S, K, f"dense 16384x{N}x{K} ({R} rows)", model)
+    check(np.ascontiguousarray(out[rows, :N]), ref32, S, K, f"dense 16384x{N}x{K} ({R} rows)", model, window)
     assert np.all(out[rows, N:] == 0xc0e0)                                     # bf16 -7.0 past n untouched
 
 
@@ -181,11 +183,13 @@ def test_fp8_gemm_psum(n, k):
     counts, psum, rows, a, sfa, w, sfb = grouped_case(T, n, k, seed=n + k)
     ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, 256, n, k, rows, k, rows, abs_too=True)
     model = ref.fp8_gemm_psum_mfma(a, w, sfa, sfb, psum, 256, n, k, rows, k, rows)
+    window = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, 256, n, k, rows, k, rows)
     c = filled((rows, n), SENTINEL, torch.int16)
     ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows)
     out = h(c, np.uint16)
     owned = ~torch.isnan(ref32[:, 0]).numpy()
-    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum n={n} k={k}", model[owned])
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum n={n} k={k}", model[owned],
+          window[owned])
     assert np.all(out[~owned] == SENTINEL)
 
 
@@ -205,12 +209,14 @@ def test_fp8_gemm_psum_groups(groups, seed):
     w, sfb = quant_weight(n, k, seed=seed + 1, groups=groups)
     ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows, abs_too=True)
     model = ref.fp8_gemm_psum_mfma(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
+    window = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
     c = filled((rows, n), SENTINEL, torch.int16)
     ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows,
                       groups=groups)
     out = h(c, np.uint16)
     owned = ~torch.isnan(ref32[:, 0]).numpy()
-    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum groups={groups}", model[owned])
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum groups={groups}", model[owned],
+          window[owned])
     assert np.all(out[~owned] == SENTINEL)
 
 
@@ -351,6 +357,25 @@ def test_bf16_batched_bench_shapes_sampled():
                      b_strides=(1024, 458752), d_strides=(32768, 512))
     B = kvb.view(64, 448, 512)[:, 192:448, :].cpu()
     bf16_ref_check(h(ov[rows].contiguous().view(torch.int16), np.uint16), o[rows].cpu(), B, 512, "uv 16384")
+
+
+def test_bf16_batched_k128_bench_shape_sampled():
+    """BASELINE's W_UK statement at full size: 64 heads x [16384 x 128] . [128 x 512], contiguous operands (the
+    bench's aux.w_uk_k128_bf16_batched launch); tile-edge and random rows of every head against the oracle,
+    every column, and the rows past m untouched."""
+    M, rows = 16384, 16384 + 64
+    print("bf16 batched 16384 rows x 64 heads, K 128", flush=True)
+    g = synth.generator(46, "cuda")
+    A = torch.randn(rows, 64, 128, generator=g, device=DEV).to(torch.bfloat16)
+    B = (torch.randn(64, 512, 128, generator=g, device=DEV) * 0.1).to(torch.bfloat16)
+    D = torch.full((rows, 64, 512), -3.0, dtype=torch.bfloat16, device=DEV)
+    ops.bf16_batched(A, B, D, M, n=512, k=128, rows=rows, a_strides=(64 * 256, 256), b_strides=(256, 512 * 256),
+                     d_strides=(64 * 1024, 1024))
+    sample = sorted({0, 1, 127, 128, 255, 256, 8191, 8192, M - 2, M - 1} |
+                    set(np.random.default_rng(7).choice(M, 8, replace=False).tolist()))
+    bf16_ref_check(h(D[sample].contiguous().view(torch.int16), np.uint16), A[sample].cpu(), B.cpu(), 128,
+                   f"k128 16384 ({len(sample)} rows)")
+    assert bool((D[M:] == -3.0).all())
 
 
 def test_bf16_batched_contiguous_k128():

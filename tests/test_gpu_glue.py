@@ -77,6 +77,39 @@ def test_silu_mul_quant_bit_exact(rows, I, n, sf_rows):
     assert np.array_equal(h(sf, np.uint8), sf_ref)
 
 
+@pytest.mark.parametrize("rows,I", [(256, 2048), (64, 12288)])
+def test_silu_mul_quant_against_ieee_silu(rows, I):
+    """Against a chain that does not share the library's SiLU: float64 SiLU rounded to f32, the f32 product with
+    the up value, bf16, then the oracle's (bit-exact) quant.  The two SiLUs differ by a few f32 ulp, which moves
+    bf16(silu(g) u) by one bf16 ulp now and then and a code by one e4m3 step more rarely: the codes must agree
+    on >= 99.9% of the elements, and every code that differs must be one step off under the same scale byte."""
+    g = synth.generator(7 * rows + I)
+    gu = bf16_bits((torch.randn(rows, 2 * I, generator=g) * 4).to(torch.bfloat16))
+    q = filled((rows, I), 0)
+    sf = filled((ref.sf_words(I) * rows * 4,), 0)
+    ops.silu_mul_quant(d(gu), I, q, sf, rows, None, rows)
+    gate = ref.bf16_to_f32(gu[:, :I]).astype(np.float64)
+    up = ref.bf16_to_f32(gu[:, I:])
+    with np.errstate(over="ignore"):
+        silu = (gate / (1.0 + np.exp(-gate))).astype(np.float32)
+    v = ref.bf16_round((silu * up).astype(np.float32))
+    q_ind, sf_ind = ref.quant(v, I, rows)
+    qk, sfk = h(q, np.uint8), h(sf, np.uint8)
+    same_sf = sfk.reshape(-1, rows, 4).transpose(1, 0, 2).reshape(rows, -1) == \
+        sf_ind.reshape(-1, rows, 4).transpose(1, 0, 2).reshape(rows, -1)
+    assert same_sf.mean() >= 0.999, f"scale bytes equal on {same_sf.mean():.5f} of the blocks"
+    blk = np.repeat(same_sf[:, :I // 128], 128, axis=1)
+    eq = qk == q_ind
+    step = np.abs(ref.e4m3_decode(qk).astype(np.float64) - ref.e4m3_decode(q_ind).astype(np.float64))
+    mag = np.maximum(np.abs(ref.e4m3_decode(qk)), np.abs(ref.e4m3_decode(q_ind))).astype(np.float64)
+    # one e4m3 step at |x|: 2^(floor(log2 |x|) - 3) for normals (>= 2^-6), 2^-9 below
+    one = np.where(mag >= 2.0 ** -6, np.exp2(np.floor(np.log2(np.maximum(mag, 2.0 ** -6))) - 3), 2.0 ** -9)
+    print(f"silu_mul_quant vs an IEEE SiLU chain ({rows}x{I}): {eq.mean() * 100:.4f}% of codes equal, "
+          f"{same_sf.mean() * 100:.3f}% of scale bytes", flush=True)
+    assert eq.mean() >= 0.999
+    assert np.all(step[blk & ~eq] <= one[blk & ~eq] * (1 + 2.0 ** -20))
+
+
 # ------------------------------------------------------------------ routing, psum (a6, a7)
 
 def zipf_ids(T, seed):

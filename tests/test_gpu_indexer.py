@@ -134,7 +134,8 @@ def paged(rng, seq_lens, n_pages):
     return bt
 
 
-@pytest.mark.parametrize("seq_lens", [[130, 64, 1, 200], [65536], [1000, 1, 63, 65, 4097]])
+@pytest.mark.parametrize("seq_lens", [[130, 64, 1, 200], [65536], [1000, 1, 63, 65, 4097],
+                                      [(i * 37) % 150 for i in range(70)]])    # 70 sequences, empty ones among them
 def test_idx_gather_and_kv_dequant_bit_exact(seq_lens):
     print(f"idx_gather / kv_dequant seq_lens={seq_lens}", flush=True)
     rng = np.random.default_rng(sum(seq_lens))

@@ -38,9 +38,11 @@ def silu_quant_dequant(g_bits, I):
     return ref.dequant(torch.from_numpy(q), ref.scale_exponents(sf, rows, I)).to(DEV)
 
 
-def test_moe_block_against_oracle_chain():
-    T, x_rows = 512, 512
-    print(f"moe block T={T}", flush=True)
+@pytest.mark.parametrize("T,x_rows", [(512, 512), (400, 400)])
+def test_moe_block_against_oracle_chain(T, x_rows):
+    """(400, 400): a chunk of rows not a multiple of 128, whose shared expert takes the dense GEMM + silu_mul_quant
+    pair rather than the fused grouped GEMM (which needs x_rows in 128-row blocks)."""
+    print(f"moe block T={T} x_rows={x_rows}", flush=True)
     g = synth.generator(41, "cuda")
     xn = synth.activations(T, H, g, device=DEV)
     xq = torch.empty(T, H, dtype=torch.uint8, device=DEV)
@@ -56,6 +58,7 @@ def test_moe_block_against_oracle_chain():
     w_sdn, sf_sdn = requant_groups(1, H, INTER, 950)
     W = moe.MoEWeights(w_r, bias, rs, w13, sf13, w2, sf2, w_sgu, sf_sgu, w_sdn, sf_sdn)
     B = moe.MoEBuffers(T, x_rows, DEV)
+    assert B.fused_shared == (x_rows % 128 == 0)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
     moe.moe_block(xn, xq, xsf, W, B, out)
     torch.cuda.synchronize()

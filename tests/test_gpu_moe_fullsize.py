@@ -27,7 +27,7 @@ def scale_bytes(g, n):
 
 
 def oracle_rows(a, sfa, rows_all, w, sfb, e, n, k, sample):
-    """f32 reference, abs-sum and MFMA-model sum of `sample` rows (all owned by expert e)."""
+    """f32 reference, abs-sum, MFMA-model sum and MFMA window bound of `sample` rows (all owned by expert e)."""
     kw = ref.sf_words(k)
     a_s = h(a[sample], np.uint8)
     sfa_s = np.ascontiguousarray(h(sfa, np.uint8).reshape(-1, rows_all, 4)[:, sample, :]).reshape(-1)
@@ -35,7 +35,8 @@ def oracle_rows(a, sfa, rows_all, w, sfb, e, n, k, sample):
     sfb_e = h(sfb[e * kw * n * 4:(e + 1) * kw * n * 4], np.uint8)
     R = len(sample)
     return (ref.fp8_gemm(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R), ref.fp8_gemm_abs(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R),
-            ref.fp8_gemm_mfma(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R))
+            ref.fp8_gemm_mfma(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R),
+            ref.fp8_window_bound(a_s, w_e, sfa_s, sfb_e, R, n, k, k, R))
 
 
 def test_moe_gemms_full_size():
@@ -88,7 +89,7 @@ def test_moe_gemms_full_size():
         s0, s1 = ranges[e]
         sample = sorted({s0, s1 - 1, (s0 + s1) // 2, s0 + (s1 - s0 - 1) // 256 * 256})   # + the last tile's first
         print(f"expert {e}: rows [{s0}, {s1}), sampled {sample}", flush=True)
-        r32, S, Wb = oracle_rows(mq, msf, rows, w13, sf13, e, 2 * INTER, H, sample)
-        check(h(g13[sample].view(torch.int16), np.uint16), r32, S, H, f"gate_up expert {e}", Wb)
-        r32, S, Wb = oracle_rows(q2, sf2, rows, wd, sfd, e, H, INTER, sample)
-        check(h(f2[sample].view(torch.int16), np.uint16), r32, S, INTER, f"down expert {e}", Wb)
+        r32, S, Wb, win = oracle_rows(mq, msf, rows, w13, sf13, e, 2 * INTER, H, sample)
+        check(h(g13[sample].view(torch.int16), np.uint16), r32, S, H, f"gate_up expert {e}", Wb, win)
+        r32, S, Wb, win = oracle_rows(q2, sf2, rows, wd, sfd, e, H, INTER, sample)
+        check(h(f2[sample].view(torch.int16), np.uint16), r32, S, INTER, f"down expert {e}", Wb, win)

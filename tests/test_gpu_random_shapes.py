@@ -39,10 +39,11 @@ def test_fp8_gemm_random(M, N, K, rows, lda, ldc, sfa_rows):
     ref32 = ref.fp8_gemm(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
     S = ref.fp8_gemm_abs(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
     model = model_on_rows(a, w, sfa, sfb, M, N, K, lda, sfa_rows, sample_rows(M, seed=M))
+    window = ref.fp8_window_bound(a, w, sfa, sfb, M, N, K, lda, sfa_rows)
     c = filled((rows, ldc), SENTINEL, torch.int16)
     ops.fp8_gemm(d(a), d(w), d(sfa), d(sfb), c, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
     out = h(c, np.uint16)
-    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"random {M}x{N}x{K}", model)
+    check(np.ascontiguousarray(out[:M, :N]), ref32, S, K, f"random {M}x{N}x{K}", model, window)
     assert np.all(out[:M, N:] == SENTINEL) and np.all(out[M:] == SENTINEL)
 
 
@@ -59,12 +60,14 @@ def test_fp8_gemm_psum_random(seed):
     w, sfb = quant_weight(n, k, seed=seed + 41, groups=groups)
     ref32, S = ref.fp8_gemm_psum(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows, abs_too=True)
     model = ref.fp8_gemm_psum_mfma(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
+    window = ref.fp8_gemm_psum_window(a, w, sfa, sfb, psum, groups, n, k, rows, k, rows)
     c = filled((rows, n), SENTINEL, torch.int16)
     ops.fp8_gemm_psum(d(a), d(w), d(sfa), d(sfb), c, d(psum), n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows,
                       groups=groups)
     out = h(c, np.uint16)
     owned = ~torch.isnan(ref32[:, 0]).numpy()
-    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum seed={seed}", model[owned])
+    check(np.ascontiguousarray(out[owned]), ref32[owned], S[owned], k, f"psum seed={seed}", model[owned],
+          window[owned])
     assert np.all(out[~owned] == SENTINEL)
 
 

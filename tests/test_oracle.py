@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from kern_glm53_amd import synth
 from oracle import ref
 
 
@@ -538,3 +539,31 @@ def test_fp8_window_bound_brute_force():
             want = sum(np.abs(da[m, g * 64:(g + 1) * 64]).max() * np.abs(dw[n, g * 64:(g + 1) * 64]).max()
                        for g in range(K // 64))
             assert abs(B[m, n] - want) <= 1e-12 * want
+
+
+def test_window_bar_passes_the_model_and_catches_a_scale_byte():
+    """The per-element bar the fp8 GEMM tests apply to every element (2 bf16 ulp + order noise + 2^-7 x the
+    MFMA window bound) holds for the oracle's model of the instruction (what the kernels compute), and fails
+    when one 128-K block of one activation row uses a scale exponent one too high: the per-tile mistake
+    (a wrong scale byte, a bad tail tile) that the sampled-row model check alone could miss."""
+    rng = np.random.default_rng(23)
+    M, N, K = 8, 64, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, rng.choice(K, 5, replace=False)] *= 50
+    xb = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    a, sfa = ref.quant(xb, K, M)
+    w8, s = synth.weights(N, K, synth.generator(5))
+    wq = np.zeros((N, K), np.uint8)
+    sfb = np.zeros(ref.sf_words(K) * N * 4, np.uint8)
+    ref.requant(w8.numpy(), s.numpy(), wq, sfb, N, K, (N + 127) // 128 * 128, 0, 0, N, 0)
+    ref32 = ref.fp8_gemm(a, wq, sfa, sfb, M, N, K, K, M)
+    S = ref.fp8_gemm_abs(a, wq, sfa, sfb, M, N, K, K, M)
+    window = ref.fp8_window_bound(a, wq, sfa, sfb, M, N, K, K, M)
+    model = torch.from_numpy(ref.fp8_gemm_mfma(a, wq, sfa, sfb, M, N, K, K, M))
+    ok, rep = ref.check_bf16_gemm(model.to(torch.bfloat16).float(), ref32, S, K, window=window)
+    assert ok and rep["n_over_window"] == 0, ref.parity_line("model", rep)
+    bad_sfa = sfa.copy()
+    bad_sfa[(0 * M + 3) * 4 + 2] += 1            # row 3, K block 2 (word 0, byte 2): that block's products x 2
+    bad = torch.from_numpy(ref.fp8_gemm_mfma(a, wq, bad_sfa, sfb, M, N, K, K, M))
+    ok, rep = ref.check_bf16_gemm(bad.to(torch.bfloat16).float(), ref32, S, K, window=window)
+    assert not ok and rep["n_over_window"] > 0
