@@ -401,6 +401,108 @@ def time_launch(fn, stream, iters=7):
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in ev)
 
 
+def sclk_files():
+    """The sysfs DPM tables of the box's GPUs (`pp_dpm_sclk`: one line per level, the current one marked '*')."""
+    import glob
+    return sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+
+
+def read_sclk(path):
+    """The current shader clock (MHz) of a pp_dpm_sclk table, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.rstrip().endswith("*"):
+                    return int(line.split(":")[1].strip().lower().split("mhz")[0])
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
+
+
+def clock_leg(L, seconds=1.0, period=0.002):
+    """The shader clock while the step's GEMMs run: the five launches loop for `seconds` (the same load as the
+    timed steps, right after them) while a thread reads the GPU's sysfs DPM table every `period` s."""
+    import threading
+    files = sclk_files()
+    if not files:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            v = read_sclk(files[0])
+            if v is not None:
+                samples.append(v)
+            time.sleep(period)
+
+    th = threading.Thread(target=sampler, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    while time.perf_counter() - t0 < seconds:
+        for _, _, fn in L:
+            fn()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    if not samples:
+        return None
+    return {"mhz_median": int(statistics.median(samples)), "mhz_min": min(samples), "mhz_max": max(samples),
+            "samples": len(samples), "source": f"{files[0]} (current DPM level), sampled every "
+                                               f"{period * 1e3:.0f} ms while the five GEMMs loop for {seconds:.1f} s"}
+
+
+def mfma_ceiling(dev, iters=20000, warm=4, runs=5):
+    """libkg_probe.so's MFMA-only loop (v_mfma_scale_f32_32x32x64_f8f6f4 on random e4m3 register operands, one
+    4-wave workgroup per CU): TFLOP/s (median of `runs` launches after `warm`) and the shader clock it ran at
+    (s_memtime cycles over s_memrealtime's 100 MHz ticks, median over the workgroups)."""
+    import ctypes
+    from kern_glm53_amd import build as kbuild
+    lib = ctypes.CDLL(str(kbuild.PROBE_LIB))
+    lib.kg_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint, ctypes.c_void_p, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(grid * 256, dtype=torch.float32, device=dev)
+    clocks = torch.zeros(grid, 2, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream()
+    ms, mhz = [], []
+    for i in range(warm + runs):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rc = lib.kg_probe_mfma(grid, iters, 1234 + i, sink.data_ptr(), clocks.data_ptr(), stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        assert rc == 0, f"kg_probe_mfma: hipError_t {rc}"
+        if i >= warm:
+            ms.append(e0.elapsed_time(e1))
+            c = clocks.cpu().double()
+            mhz.append(float((c[:, 0] / c[:, 1]).median()) * 100.0)
+    flops = grid * 4 * iters * 8 * 2.0 * 32 * 32 * 64
+    t = statistics.median(ms)
+    return {"tflops": round(flops / (t * 1e-3) / 1e12, 1), "ms": round(t, 3), "clock_mhz": round(statistics.median(mhz)),
+            "what": "v_mfma_scale_f32_32x32x64_f8f6f4 back to back on per-lane random e4m3 register operands, "
+                    f"8 accumulators a wave, 4 waves x {grid} workgroups, {iters} trips, no memory or LDS traffic"}
+
+
+def scaled_mm_leg(dev, iters=7):
+    """torch._scaled_mm (hipBLASLt's fp8 GEMM with per-tensor scales, no 128-block scales) at the three dense
+    shapes, for scale: median ms and TFLOP/s, or the error it raised."""
+    out = {}
+    for name, n, k, _ in DENSE:
+        try:
+            g = torch.Generator(device=dev)
+            g.manual_seed(n + k)
+            a = (torch.randn(M, k, generator=g, device=dev) * 0.5).to(torch.float8_e4m3fn)
+            b = (torch.randn(n, k, generator=g, device=dev) * 0.5).to(torch.float8_e4m3fn)
+            one = torch.ones((), device=dev)
+            fn = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            ms = time_launch(fn, torch.cuda.current_stream(), iters)
+            out[name] = {"ms": round(ms, 4), "tflops": round(2.0 * M * n * k / (ms * 1e-3) / 1e12, 1)}
+            del a, b
+        except Exception as ex:      # not every torch build offers fp8 _scaled_mm on this GPU
+            out[name] = {"error": f"{type(ex).__name__}: {str(ex)[:160]}"}
+    return out
+
+
 def cpu_baseline(data, aux, rows=8192, runs=5):
     """The oracle's reference math on PyTorch-CPU, three bounded legs (about 15 s in all):
       * dense: fp32 dequantize-then-matmul on rows [0, rows) of each dense GEMM (half the chunk), median of
@@ -528,6 +630,8 @@ def main():
                 "frac": round(dflops / (per[dom]["ms"] * 1e-3) / PEAK_FP8, 4), "traffic": measured_traffic(dom),
                 "kernel": dom}
     log("per kernel: " + ", ".join(f"{k} {v['ms']:.3f} ms {v['tflops']:.0f} TF/s" for k, v in per.items()))
+    sclk = clock_leg(L)
+    log(f"shader clock while the GEMMs run: {sclk}")
 
     # glue around the MoE GEMMs and the other GEMM rows of the path (not part of `value`)
     glue = {}
@@ -576,6 +680,14 @@ def main():
                                                                      + glue["moe_gather"]["us"] * 1e-3, 4)}}
     log(f"gathered gate_up: {gms:.3f} ms (gather + gate_up {variants['gate_up_gathered_silu_quant']['vs_chain_ms']:.3f} ms)")
 
+    ceiling = {"mfma_only": mfma_ceiling(dev), "scaled_mm_per_tensor": scaled_mm_leg(dev), "sclk_during_gemms": sclk,
+               "l2_mall_flushed": False,
+               "note": "kernel times are taken back to back with no L2 / MALL flush between launches; the MoE "
+                       "weights (9.7 GB) exceed the 256 MB MALL anyway, the dense operands (0.2-0.6 GB) do not"}
+    aux["mfma_ceiling_tflops"] = ceiling["mfma_only"]["tflops"]
+    log(f"ceiling: mfma-only {ceiling['mfma_only']['tflops']} TF/s at {ceiling['mfma_only']['clock_mhz']} MHz; "
+        f"scaled_mm {ceiling['scaled_mm_per_tensor']}")
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle, PyTorch-CPU)")
@@ -593,6 +705,7 @@ def main():
                        value * 1e12 / PEAK_FP8, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "ceiling": ceiling,
         "kernels": per,
         "glue": glue,
         "producers": producers,

@@ -1,4 +1,5 @@
-"""Builds `kern_glm53_amd/libkg.so` (the C-ABI library of include/kg.h) from csrc/*.hip with hipcc for gfx950.
+"""Builds `kern_glm53_amd/libkg.so` (the C-ABI library of include/kg.h) from csrc/*.hip with hipcc for gfx950,
+and `libkg_probe.so`, the benchmark's measurement kernels (csrc/kg_probe.hip: the MFMA-only ceiling).
 
     python -m kern_glm53_amd.build          # or kern_glm53_amd.build.build()
 
@@ -20,6 +21,8 @@ PKG = pathlib.Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libkg.so"
+PROBE_LIB = PKG / "libkg_probe.so"          # the benchmark's measurement kernels (not the op library)
+PROBE_SOURCE = "kg_probe.hip"
 INCLUDE = PKG.parent / "include"
 ARCH = "gfx950"
 
@@ -64,8 +67,14 @@ def build(verbose: bool = False) -> pathlib.Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *COMMON, "-shared", str(CSRC / PROBE_SOURCE), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PROBE_SOURCE}:\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB}", file=sys.stderr)
+        print(f"built {LIB} and {PROBE_LIB}", file=sys.stderr)
     return LIB
 
 
