@@ -194,20 +194,26 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
 // The manifest's library GEMMs at the layer's shapes are long in K and skinny in N: the MoE router (N = 256)
 // and the indexer's weights_proj (N = 32) over M = 16384 rows, K = 6144.  They make few tiles (256 and 128
 // of the batched kernel's 128 x 128), one per CU at most, so a single-stage workgroup leaves every load
-// exposed.  Here one workgroup per CU pipelines its own K loop: a ring of STAGES LDS stages (K = 64 each, the
-// batched kernel's swizzled 128-byte rows), the DMA of stage s + STAGES - 1 issued right after stage s's
-// barrier; 128 x 128 tiles, 4 waves of 64 x 64 (TI = TJ = 2); the column tiles of one row block are
-// consecutive, so they run on one XCD and A comes from HBM once.  (N <= 64 takes kg_gemm_ksplit_kernel below.)
+// exposed.  Here one workgroup per CU pipelines its own K loop (K = 64 a stage, the batched kernel's swizzled
+// 128-byte rows) through two LDS rings: A, the HBM stream (each row block is read by its column tiles one
+// after the other on one XCD), SA stages deep with its DMA issued SA - 1 stages ahead, and B, which every
+// workgroup reads and L2 serves, SB = 3 stages deep and 2 ahead.  At 16384 x 256 x 6144 a CU moves 1.5 MB of
+// A and 1.5 MB of B, and a ring of 4 stages for both (3 in flight) ran 90 us: about 0.96 us a stage, the time
+// HBM takes to return the 48 KB of A in flight.  7 A stages keep 96 KB of A in flight in the same 160 KB
+// (73 us).  128 x 128 tiles; f32 out with 8 waves of 64 x 32 (TI = 1, TJ = 2: 1.5x the fragment reads, but a
+// CU sustains about twice the LDS traffic with 8 waves as with 4; 69 us), bf16 out with 4 waves of 64 x 64
+// (TI = TJ = 2, the layout its staged epilogue writes).  (N <= 64 takes kg_gemm_ksplit_kernel below.)
 // Each output is one chain of v_mfma_f32_32x32x16_bf16 over K in ascending order, as in the batched kernel,
 // so the sums are bit-identical to it.  Every stage index past the last K step is still loaded, from an
 // offset past its resource (reads zeros, touches no memory), so the waits count the same every stage.
-template <bool F32OUT, int BM, int BN, int TI, int TJ, int STAGES>
+template <bool F32OUT, int BM, int BN, int TI, int TJ, int SA_, int SB_>
 __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void kg_gemm_lib_kernel(const KgBf16Args p) {
   constexpr int WR = BM / (32 * TJ), WC = BN / (32 * TI), NW = WR * WC;   // waves along rows, columns
-  constexpr int SA = BM * 128, STAGE = (BM + BN) * 128;
-  constexpr int Q = (BM + BN) / 8 / NW;                                 // DMA instructions per wave and stage
-  static_assert((BM + BN) / 8 % NW == 0 && STAGES >= 2, "DMA split");
-  __shared__ __attribute__((aligned(1024))) u8 ring[STAGES * STAGE];
+  constexpr int STA = BM * 128, STB = BN * 128;                          // bytes of an A / B stage
+  constexpr int QA = BM / 8 / NW, QB = BN / 8 / NW;                      // DMA instructions per wave and stage
+  static_assert(BM / 8 % NW == 0 && BN / 8 % NW == 0 && SB_ == 3 && SA_ > SB_, "DMA split and waits");
+  __shared__ __attribute__((aligned(1024))) u8 ringa[SA_ * STA];
+  __shared__ __attribute__((aligned(1024))) u8 ringb[SB_ * STB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -236,7 +242,7 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
   for (int s = 0; s < 4; ++s) {
     const unsigned sw = (unsigned)(((2 * s + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
     offa[s] = (unsigned)arow0 * 128u + sw;
-    offb[s] = (unsigned)SA + (unsigned)brow0 * 128u + sw;
+    offb[s] = (unsigned)brow0 * 128u + sw;
   }
 
   v16f acc[TI][TJ];
@@ -248,49 +254,35 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int KT = p.k >> 6;
-  // stage kt into ring slot `slot`: instruction q of this wave covers LDS rows 8 (wave Q + q) .. + 7 of the
-  // stage (A rows first, then B rows); K steps at or past KT read from past the resource
-  auto issue1 = [&](int slot, int kt, int q) {
-    const int ko = kt * 128;
-    const unsigned oob = kt < KT ? 0u : 0x80000000u;
-    u8* const stage = ring + slot * STAGE;
-    const int row = (wave * Q + q) * 8;
-    if (row < BM)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + row * 128), 16,
-                                               (va[q & 1] + (unsigned)row * (unsigned)p.a_rs) | oob, ko, 0, 0);
-    else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + row * 128), 16,
-                                               (vb[q & 1] + (unsigned)(row - BM) * (unsigned)p.b_rs) | oob, ko, 0, 0);
-  };
-  auto issue = [&](int slot, int kt) {
-    const int ko = kt * 128;
-    const unsigned oob = kt < KT ? 0u : 0x80000000u;
-    u8* const stage = ring + slot * STAGE;
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int row = (wave * Q + q) * 8;
-      if (row < BM)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + row * 128), 16,
-                                                 (va[q & 1] + (unsigned)row * (unsigned)p.a_rs) | oob, ko, 0, 0);
-      else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + row * 128), 16,
-                                                 (vb[q & 1] + (unsigned)(row - BM) * (unsigned)p.b_rs) | oob, ko, 0, 0);
+  // DMA instruction q of this wave for K step kt: q < QA an A instruction (rows 8 (wave QA + q) .. + 7) into A
+  // slot `as`, else a B instruction into B slot `bs`; steps at or past KT read from past the resource
+  auto issue1 = [&](int as, int akt, int bs, int bkt, int q) {
+    if (q < QA) {
+      const unsigned oob = akt < KT ? 0u : 0x80000000u;
+      const int row = (wave * QA + q) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(ringa + as * STA + row * 128), 16,
+                                               (va[q & 1] + (unsigned)row * (unsigned)p.a_rs) | oob, akt * 128, 0, 0);
+    } else {
+      const unsigned oob = bkt < KT ? 0u : 0x80000000u;
+      const int row = (wave * QB + q - QA) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(ringb + bs * STB + row * 128), 16,
+                                               (vb[q & 1] + (unsigned)row * (unsigned)p.b_rs) | oob, bkt * 128, 0, 0);
     }
   };
-  // One stage's MFMAs, with the DMA of stage nkt into slot nslot spread over them (one instruction every
-  // STEP MFMAs, kept in place by sched_barrier): issued in a burst ahead of the MFMAs, the copies and the
-  // matrix work barely overlap (the router GEMM at 16384 x 256 x 6144: 110 us that way, 90 us this way).
-  // All of the stage's fragments are read first.
-  auto compute_issue = [&](const u8* stage, int nslot, int nkt) {
+  // One stage's MFMAs, with the DMA of A step akt and B step bkt spread over them (one instruction every STEP
+  // MFMAs, kept in place by sched_barrier): issued in a burst ahead of the MFMAs, the copies and the matrix
+  // work barely overlap (the router GEMM at 16384 x 256 x 6144: 110 us that way, 90 us this way).  All of the
+  // stage's fragments are read first.
+  auto compute_issue = [&](const u8* sta, const u8* stb, int as, int akt, int bs, int bkt) {
     v8bf af[4][TI], bf[4][TJ];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int i = 0; i < TI; ++i) af[s][i] = kg_lds_bf16x8(stage + offb[s] + i * 32 * 128);
+      for (int i = 0; i < TI; ++i) af[s][i] = kg_lds_bf16x8(stb + offb[s] + i * 32 * 128);
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) bf[s][j] = kg_lds_bf16x8(stage + offa[s] + j * 32 * 128);
+      for (int j = 0; j < TJ; ++j) bf[s][j] = kg_lds_bf16x8(sta + offa[s] + j * 32 * 128);
     }
-    constexpr int NM = 4 * TI * TJ, STEP = NM / Q > 0 ? NM / Q : 1;
+    constexpr int NM = 4 * TI * TJ, Q = QA + QB, STEP = NM / Q > 0 ? NM / Q : 1;
     static_assert(NM / STEP >= Q, "every DMA instruction of the stage gets an MFMA slot");
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -300,29 +292,38 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
         for (int j = 0; j < TJ; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][i], bf[s][j], acc[i][j], 0, 0, 0);
           const int t = (s * TI + i) * TJ + j;
-          if (t % STEP == 0 && t / STEP < Q) issue1(nslot, nkt, t / STEP);
+          if (t % STEP == 0 && t / STEP < Q) issue1(as, akt, bs, bkt, t / STEP);
           __builtin_amdgcn_sched_barrier(0);
         }
   };
 
+  // Prologue: the issues of the SA - 1 stages before step 0 as the loop makes them (stage v issues A step
+  // v + SA - 1 and B step v + SB - 1), so that at every barrier the loads younger than this step's B are the
+  // QA + QB of the step before.
+  for (int v = -(SA_ - 1); v < 0; ++v) {
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
-  // stage kt: this wave's DMA of kt has landed (the STAGES - 2 younger stages may still be in flight), the
-  // barrier publishes every wave's and frees slot (kt - 1) % STAGES, into which stage kt + STAGES - 1 goes
-  int slot = 0;
-  for (int kt = 0; kt < KT; ++kt) {
-    if constexpr (STAGES == 2) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr ((STAGES - 2) * Q == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr ((STAGES - 2) * Q == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr ((STAGES - 2) * Q == 24) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr ((STAGES - 2) * Q == 32) asm volatile("s_waitcnt vmcnt(32) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr ((STAGES - 2) * Q == 40) asm volatile("s_waitcnt vmcnt(40) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else static_assert(STAGES == 2, "no wait for this ring");
-    asm volatile("" ::: "memory");
-    compute_issue(ring + slot * STAGE, slot == 0 ? STAGES - 1 : slot - 1, kt + STAGES - 1);
-    slot = slot + 1 == STAGES ? 0 : slot + 1;
+    for (int q = 0; q < QA; ++q) issue1(v + SA_ - 1, v + SA_ - 1, 0, 0, q);
+    if (v + SB_ - 1 >= 0) {
+#pragma unroll
+      for (int q = QA; q < QA + QB; ++q) issue1(0, 0, v + SB_ - 1, v + SB_ - 1, q);
+    }
   }
-  // the DMA past the last step is still writing (zeros) into the ring: drain it before staging there
+  // step kt: this wave's A and B DMA of kt have landed (the QA + QB instructions of the step before are the only
+  // younger loads, and loads complete in issue order), the barrier publishes every wave's and frees the slots of
+  // step kt - 1, into which A step kt + SA - 1 and B step kt + SB - 1 go
+  int as = 0, bs = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    if constexpr (QA + QB == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (QA + QB == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (QA + QB == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else static_assert(QA + QB == 8, "no wait for this split");
+    asm volatile("" ::: "memory");
+    const int fa = as == 0 ? SA_ - 1 : as - 1, fb = bs == 0 ? SB_ - 1 : bs - 1;     // slots of step kt - 1
+    compute_issue(ringa + as * STA, ringb + bs * STB, fa, kt + SA_ - 1, fb, kt + SB_ - 1);
+    as = as + 1 == SA_ ? 0 : as + 1;
+    bs = bs + 1 == SB_ ? 0 : bs + 1;
+  }
+  // the DMA past the last step is still writing (zeros) into the rings: drain it before staging there
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 
   if constexpr (F32OUT) {
@@ -353,7 +354,7 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
     }
   } else {
     // bf16, 128 x 128 tiles: the batched kernel's LDS-staged epilogue (whole 128-byte row pieces)
-    u8* const stg = ring + wave * 8192;
+    u8* const stg = ringa + wave * 8192;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int m = j * 32 + (lane & 31);
@@ -567,8 +568,8 @@ static int kg_gemm_lib_launch(bool f32out, const void* a, const void* b, void* c
   const long long total = (long long)p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
   const dim3 grid((unsigned)total);
-  if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 128, 128, 2, 2, 4>), grid, dim3(256), 0, st, p);
+  if (f32out) hipLaunchKernelGGL((kg_gemm_lib_kernel<true, 128, 128, 1, 2, 7, 3>), grid, dim3(512), 0, st, p);
+  else hipLaunchKernelGGL((kg_gemm_lib_kernel<false, 128, 128, 2, 2, 7, 3>), grid, dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
