@@ -668,17 +668,6 @@ def main():
                         "tiles": tiles, "us_per_tile_per_cu": round(ms * 1e3 * 256 / tiles, 2)}
     log("skinny experts: " + ", ".join(f"{k} {v['ms']:.3f} ms ({v['tflops']:.0f} TF/s, {v['gbps']:.0f} GB/s)"
                                        for k, v in skinny.items()))
-    # the gather folded into gate_up's A load, against the gather + gate_up chain the step times
-    from kern_glm53_amd import ops
-    xq, xsf = data["q_a_kv_a"]["a"], data["q_a_kv_a"]["sfa"]
-    gms = time_launch(lambda: ops.fp8_gemm_psum_gather_silu_quant(
-        xq, xsf, M, m["route_map"], m["w13"], m["sf13"], m["psum"], m["mq2"], m["msf2"], n=2 * INTER, k=H,
-        rows=m["mcap"], lda=H, sf_rows=m["mcap"]), stream)
-    gflops = 2.0 * m["R"] * 2 * INTER * H
-    variants = {"gate_up_gathered_silu_quant": {"ms": round(gms, 4), "tflops": round(gflops / (gms * 1e-3) / 1e12, 2),
-                                                "vs_chain_ms": round(per["moe_gate_up_silu_quant"]["ms"]
-                                                                     + glue["moe_gather"]["us"] * 1e-3, 4)}}
-    log(f"gathered gate_up: {gms:.3f} ms (gather + gate_up {variants['gate_up_gathered_silu_quant']['vs_chain_ms']:.3f} ms)")
 
     ceiling = {"mfma_only": mfma_ceiling(dev), "scaled_mm_per_tensor": scaled_mm_leg(dev), "sclk_during_gemms": sclk,
                "l2_mall_flushed": False,
@@ -712,7 +701,6 @@ def main():
         "moe_block": block,
         "aux": aux,
         "moe_skinny": skinny,
-        "variants": variants,
     }
     print(json.dumps(line), flush=True)
 

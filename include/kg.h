@@ -55,17 +55,6 @@ int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, c
                                 int groups, int n, int k, int rows, int lda, int sfa_rows, void* q, void* sf,
                                 int sf_rows, void* stream);
 
-/* kg_fp8_gemm_psum_silu_quant with the gather folded into the A operand's load: the grouped operand's row r is
- * token row x[route_map[r]] (e4m3 [x_rows][lda]) with scale words xsf[w][route_map[r]] ([kw][x_rows]), so the
- * gathered copy (`mq`, `msf` of glm_moe_gather, source/glm_glue.cu:463-475; scripts/gen.py:440-442) is never
- * written.  route_map: the routing's [rows] permuted-row -> token map (kg_moe_routing); only rows a group
- * owns are read.  Same outputs, bit for bit, as kg_moe_gather followed by kg_fp8_gemm_psum_silu_quant.  Has no
- * single counterpart in the reference (it fuses two of its ops).  Requires x_rows * lda below 2^31 and the
- * fused variant's other limits. */
-int kg_fp8_gemm_psum_gather_silu_quant(const void* x, const void* xsf, int x_rows, const int* route_map,
-                                       const void* w, const void* sfb, const int* psum, int groups, int n, int k,
-                                       int rows, int lda, void* q, void* sf, int sf_rows, void* stream);
-
 /* bf16 GEMM batched over heads.  Replaces `bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:88-99;
  * instance source/glm_deepgemm.cu:42-43):  D[r][h][0:n] = bf16(sum_k A[r][h][k] B[h][d][k]), f32
  * accumulation, r < m, h < heads.  Every operand is a byte-strided view: element (r, h, x) of A at

@@ -34,10 +34,8 @@ struct KgFp8Args {
   u16* c;            // bf16 [rows][ldc]           (modes 0, 1)
   const int* psum;   // int [groups]               (modes 1, 2)
   u8* q;             // e4m3 [rows][n / 2]         (mode 2)
-  u8* qsf;           // words [n / 1024][sf_rows]  (modes 2, 3)
-  const int* rmap;   // int [rows]: row -> A row   (mode 3: the gather's route_map)
+  u8* qsf;           // words [n / 1024][sf_rows]  (mode 2)
   int m, n, k, rows, lda, ldc, sfa_rows, groups, sf_rows;
-  int a_rows;        // rows of A (mode 3: the token rows; else rows)
   int m_tiles, n_tiles;
 };
 
@@ -350,7 +348,6 @@ __global__ __launch_bounds__(256, 2) void kg_fp8_gemm_tile(const KgFp8Args p) {
 
 struct KgPTile {                      // one tile (wave-uniform)
   int m0, m_end, nt, g;
-  int tb;                             // mode 3: its slot of the row table (the tile's round & 1)
 };
 
 // Tile idx (< live) -> its rows, column tile and expert.  Tiles come in groups of G row tiles, column-major
@@ -397,7 +394,6 @@ struct KgDmaSrc {
   __amdgpu_buffer_rsrc_t rw;
   unsigned abase, wbase;
   int half;                                    // a tile of at most 128 rows: A rows 128.. are not loaded
-  int tb;                                      // mode 3: the tile's slot of the row table
 };
 
 KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
@@ -407,7 +403,6 @@ KG_DEV KgDmaSrc kg_dma_src(const KgFp8Args& p, const KgPTile& t, int cn) {
   d.abase = ok ? (unsigned)(t.m0 * p.lda) : KG_OOB;
   d.wbase = (unsigned)(t.nt * cn * p.k);
   d.half = t.m_end - t.m0 <= 128;
-  d.tb = t.tb;
   return d;
 }
 
@@ -546,8 +541,7 @@ KG_DEV int kg_round_tile(int r, int live) {
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args p) {
   constexpr int BM = 256, BN = 256, TI = 4, TJ = 4, NO = 4, NI = 4, NIH = 2, SA = 256 * 128, STAGE = 512 * 128;
-  constexpr bool FUSED = MODE >= 2;           // the SiLU-mul-quant epilogue (mode 3 also gathers A)
-  constexpr bool GATHER = MODE == 3;
+  constexpr bool FUSED = MODE >= 2;           // the SiLU-mul-quant epilogue
   constexpr int CN = FUSED ? 128 : 256;   // output columns (of n) per column tile
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
@@ -555,9 +549,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   __shared__ float xam[FUSED ? 2 : 1][BM];
   __shared__ u8 xe[FUSED ? BM : 1];
   __shared__ __attribute__((aligned(1024))) u8 stg[FUSED ? 16 : 16384];   // modes 0/1 epilogue staging
-  // mode 3: A row (token) of each of the tile's 256 rows, -1 past its live rows; slot round & 1 holds the
-  // tile of that parity, so the next tile's table is written while this tile's is read
-  __shared__ int rowt[GATHER ? 2 : 1][GATHER ? BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -613,13 +604,8 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   const int KS = ((p.k + 511) >> 9) << 2;      // stages per tile (padded to a multiple of 4)
   const int KB = p.k >> 7;                     // live K blocks of 128
   const int half = p.n >> 1, kw = (p.k + 511) >> 9;
-  const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a, (long long)p.a_rows * p.lda);
+  const __amdgpu_buffer_rsrc_t ra = kg_rsrc(p.a, (long long)p.rows * p.lda);
   const __amdgpu_buffer_rsrc_t rsa = kg_rsrc(p.sfa, (long long)kw * p.sfa_rows * 4);
-  // mode 3: this thread's entry of tile t's row table (route_map of its row, -1 past the live rows)
-  auto row_of = [&](const KgPTile& t) -> int {
-    const int r = t.m0 + tid;
-    return t.g >= 0 && r < t.m_end ? p.rmap[r] : -1;
-  };
 
   // Per-lane DMA offsets: instruction q (0..7) of this wave covers tile rows 8 (8 wave + q) .. + 7, lane l
   // row + (l >> 3) and the chunk that belongs in LDS slot l & 7: (l & 7) ^ (4 (q & 1) + (l >> 4)).
@@ -666,16 +652,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     const int q = MODE == 2 ? qi ^ 8 : qi;
     const int j = q & 7;
     unsigned v;
-    if (GATHER && q < 8) {
-      // mode 3: lane l's row 64 wave + 8 j + (l >> 3) of the tile is A row rowt[tb][..] (or none), its chunk
-      // the slot's; the immediate offset is taken off as below
-      // (the lane id formed here keeps the table read at this instruction rather than hoisted)
-      const int ln = kg_lane_here();
-      const int tok = rowt[d.tb][wave * 64 + j * 8 + (ln >> 3)];
-      const bool none = tok < 0 || (d.half && wave >= 2) || ko >= p.k;
-      const unsigned chunk = (unsigned)(((ln & 7) ^ (((j & 1) << 2) | (ln >> 4))) << 4);
-      v = (none ? KG_OOB : (unsigned)tok * (unsigned)p.lda) + chunk - (unsigned)((j & 3) * 1024);
-    } else {
+    {
       unsigned u = q < 8 ? (d.half && wave >= 2 ? KG_OOB : arow_w + d.abase) : wrow_w + d.wbase;
       if (ko >= p.k) u = KG_OOB;
       // The lane offset passes through an empty asm statement, so that the compiler forms the VGPR offset
@@ -718,15 +695,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     const int arow0 = wm * (BM / 2) + (ln & 31);
     const int arow = t.m_end - t.m0 <= 128 ? arow0 - wm * 64 : arow0;   // a half tile's wave rows
     const int n0 = t.nt * CN;
-    if constexpr (GATHER) {
-      // the scale words of the rows' A rows (-1: none, read as zero, never used)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int tok = rowt[t.tb][arow + 32 * j];
-        const unsigned off = tok < 0 ? KG_OOB : (unsigned)((tok + kg4 * p.sfa_rows) * 4);
-        xa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, off, 0, 0);
-      }
-    } else {
+    {
       const unsigned sa_off = (unsigned)((t.m0 + arow) * 4 + kg4 * p.sfa_rows * 4);
 #pragma unroll
       for (int j = 0; j < TJ; ++j) xa[j] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_off + j * 128, 0, 0);
@@ -762,7 +731,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // modes 0/1 ran 3-10% slower.  Mode 2 swaps the two halves (the weight rows, its HBM stream, right after
   // the barrier: gate_up 0.7% faster; the same swap ran the down GEMM 2% slower).  (The fused epilogue stages
   // its codes in the half of the last stage's buffer that the ring refills only during the next tile's first
-  // stage: the A rows in mode 2, the weight rows in mode 3.  The compiler makes an epilogue's first LDS write
+  // stage (the A rows in mode 2).  The compiler makes an epilogue's first LDS write
   // wait for all DMA in flight, as it cannot tell the DMA's LDS destination from the epilogue's.)
   constexpr int NPRE = 8;
   // A stage's barrier: this wave's DMA of stage s + 1 has landed (everything but, on PH 2, the 8 scale words
@@ -788,7 +757,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // of stage s + 1 (vmcnt 0; 8 on PH 2, whose next group's 8 scale words go out at slot 16 after it),
   // publishes it and frees CUR: slots 26..31 issue instructions 0..7 of stage s + 2 into CUR (D2 / K2),
   // slots 26..30 read stage s + 1's first fragments from OTH.
-#define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                     \
+#define KG_PSTAGE(CUR, OTH, PH, D1, K1, D2, K2)                                                            \
   do {                                                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
     _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
@@ -808,7 +777,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
           if (t_ == 25) KG_STAGE_BARRIER(PH);                                                              \
-          if (GATHER && (FIRST) && t_ == 25) rowt[nxt.tb][tid] = rown;                                     \
           if (t_ >= 26) {                                                                                 \
             _Pragma("unroll") for (int q_ = 0; q_ < 16; ++q_)                                              \
               if (q_ < NPRE && q_ * 6 / NPRE == t_ - 26) dma1(CUR, D2, K2, q_);                            \
@@ -829,7 +797,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   // t = 8 kh + 2 o + n.  The same 16 DMA instructions per stage: 8..15 of stage s + 1 in slots 0..3 (two
   // per slot), 0..7 of stage s + 2 in slots 14, 15 (four per slot); the last read of CUR is at slot 12, the barrier
   // after slot 13; the words go out at slot 6 of PH 2.
-#define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2, FIRST)                                                    \
+#define KG_PSTAGEH(CUR, OTH, PH, D1, K1, D2, K2)                                                           \
   do {                                                                                                    \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
     _Pragma("unroll") for (int kh = 0; kh < 2; ++kh) {                                                     \
@@ -852,7 +820,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
           if (n == 0 && o + 1 < NO) str[(o + 1) & 1] = KG_PFRAG_W(CUR, kh, o + 1);                         \
           if (kh == 0 && o == NO - 1 && n == 0) str[0] = KG_PFRAG_W(CUR, 1, 0);                            \
           if (t_ == 13) KG_STAGE_BARRIER(PH);                                                              \
-          if (GATHER && (FIRST) && t_ == 13) rowt[nxt.tb][tid] = rown;                                     \
           if (t_ >= 14) {                                                                                 \
             _Pragma("unroll") for (int q_ = 0; q_ < NPRE / 2; ++q_)                                        \
               dma1(CUR, D2, K2, (t_ - 14) * (NPRE / 2) + q_);                                             \
@@ -869,17 +836,11 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   } while (0)
 
   KgPTile cur = kg_ptile<MODE>(p, tp, ps, total, idx);
-  cur.tb = 0;
   int nidx = kg_round_tile(round + 1, live);
   // the next tile (g = -1 when there is none: its loads read zeros)
   KgPTile nxt = cur;
   nxt.g = -1;
   if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
-  nxt.tb = 1;
-  if constexpr (GATHER) {
-    rowt[0][tid] = row_of(cur);
-    __syncthreads();
-  }
 
   // ---- prologue: the first word group, stage 0 and instructions 0..7 of stage 1 (as the ring has them
   // at a stage's start)
@@ -894,9 +855,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 
   for (;;) {
-    // mode 3: the next tile's row table entry, loaded now and written after this tile's first barrier (which
-    // waits for every load in flight), into the slot the previous tile's table held
-    const int rown = GATHER ? row_of(nxt) : 0;
     const bool halft = cur.m_end - cur.m0 <= 128;
     // stage 0's first fragments (buffer 0 holds the tile's stage 0, published by the last barrier; read
     // here because the previous tile may have had the other shape)
@@ -935,49 +893,48 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
   _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                      \
   _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i]
     if (halft) {
-      {                                          // the first group (mode 3: the next row table at its barrier)
+      {                                          // the first group
         const int ks = 0;
         KG_GROUP_START();
-        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
-        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
-        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
-        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
       for (int ks = 4; ks < KS; ks += 4) {
         KG_GROUP_START();
-        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 0);
-        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
-        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
-        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_PSTAGEH(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGEH(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGEH(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGEH(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
     } else {
-      {                                          // the first group (mode 3: the next row table at its barrier)
+      {                                          // the first group
         const int ks = 0;
         KG_GROUP_START();
-        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 1);
-        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
-        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
-        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
       for (int ks = 4; ks < KS; ks += 4) {
         KG_GROUP_START();
-        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256, 0);
-        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384, 0);
-        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn, 0);
-        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128, 0);
+        KG_PSTAGE(st0, st1, 0, dsc, k0 + 128, dsc, k0 + 256);
+        KG_PSTAGE(st1, st0, 1, dsc, k0 + 256, dsc, k0 + 384);
+        KG_PSTAGE(st0, st1, 2, dsc, k0 + 384, dsn, kn);
+        KG_PSTAGE(st1, st0, 3, dsn, kn, dsn, kn + 128);
         KG_GROUP_END();
       }
     }
 #undef KG_GROUP_START
 #undef KG_GROUP_END
     if constexpr (FUSED) {
-      // mode 2 stages in the A rows of the last stage's buffer (it issues the weight rows after a barrier
-      // and the A rows during the next stage), mode 3 in its weight rows (the other order)
-      kg_fp8_epilogue_silu(p, acc, MODE == 2 ? st1 : st1 + SA, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn,
-                           halft);
+      // staged in the A rows of the last stage's buffer (mode 2 issues the weight rows after a barrier and
+      // the A rows during the next stage)
+      kg_fp8_epilogue_silu(p, acc, st1, xam, xe, wave, cur.m0, cur.m_end, cur.nt, wm, wn, halft);
     } else {
       // the stores drain during the next tile's first stage (its barrier waits for them)
       kg_fp8_epilogue_lds(p, acc, stg + wave * 4096, cur.m0, cur.m_end, cur.nt * CN, wm, wn, halft);
@@ -989,7 +946,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
     nidx = kg_round_tile(round + 1, live);
     nxt.g = -1;
     if (nidx >= 0) nxt = kg_ptile<MODE>(p, tp, ps, total, nidx);
-    nxt.tb = (round + 1) & 1;
     dnx = dsrc(nxt);
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -1007,7 +963,6 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_persistent(const KgFp8Args
 template __global__ void kg_fp8_gemm_persistent<0>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_persistent<1>(const KgFp8Args);
 template __global__ void kg_fp8_gemm_persistent<2>(const KgFp8Args);
-template __global__ void kg_fp8_gemm_persistent<3>(const KgFp8Args);
 
 static int kg_fp8_launch_tile(KgFp8Args& p, int total, hipStream_t st) {
   hipLaunchKernelGGL(kg_fp8_gemm_tile, dim3(total), dim3(256), 0, st, p);
@@ -1048,7 +1003,7 @@ extern "C" int kg_fp8_gemm(const void* a, const void* w, const void* sfa, const 
   if (m == 0) return 0;
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
-  p.m = m, p.n = n, p.k = k, p.rows = rows, p.a_rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows, p.groups = 1;
+  p.m = m, p.n = n, p.k = k, p.rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows, p.groups = 1;
   hipStream_t st = (hipStream_t)stream;
   const long long big = (long long)((m + 255) / 256) * ((n + 255) / 256);
   // the persistent kernel's epilogue stores 16-byte chunks of 8 columns
@@ -1074,7 +1029,7 @@ extern "C" int kg_fp8_gemm_psum(const void* a, const void* w, const void* sfa, c
   KG_CHECK((long long)((k + 511) >> 9) * sfa_rows * 4 < (1ll << 31) && (long long)((k + 511) >> 9) * n * 4 < (1ll << 31));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb, p.c = (u16*)c;
-  p.psum = psum, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.a_rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows;
+  p.psum = psum, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda, p.ldc = ldc, p.sfa_rows = sfa_rows;
   p.groups = groups;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n + 255) / 256;   // an upper bound of the live tiles
   const long long total = (long long)p.m_tiles * p.n_tiles;
@@ -1096,7 +1051,7 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   KG_CHECK((long long)((n / 2 + 511) >> 9) * sf_rows * 4 < (1ll << 31));
   KgFp8Args p{};
   p.a = (const u8*)a, p.w = (const u8*)w, p.sfa = (const u32*)sfa, p.sfb = (const u32*)sfb;
-  p.psum = psum, p.q = (u8*)q, p.qsf = (u8*)sf, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.a_rows = rows, p.lda = lda;
+  p.psum = psum, p.q = (u8*)q, p.qsf = (u8*)sf, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.lda = lda;
   p.ldc = n, p.sfa_rows = sfa_rows, p.groups = groups, p.sf_rows = sf_rows;
   p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n / 2) / 128;
   const long long total = (long long)p.m_tiles * p.n_tiles;
@@ -1105,27 +1060,3 @@ extern "C" int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const v
   return kg_fp8_launch_persistent<2>(p, total, (hipStream_t)stream);
 }
 
-// The fused SiLU-mul-quant m-grouped GEMM reading its A rows through the routing's route_map instead of a
-// gathered copy: row r of the grouped operand is x[route_map[r]] with scale words xsf[.][route_map[r]].
-extern "C" int kg_fp8_gemm_psum_gather_silu_quant(const void* x, const void* xsf, int x_rows, const int* route_map,
-                                                  const void* w, const void* sfb, const int* psum, int groups, int n,
-                                                  int k, int rows, int lda, void* q, void* sf, int sf_rows,
-                                                  void* stream) {
-  KG_CHECK(x && xsf && route_map && w && sfb && psum && q && sf && groups >= 1 && groups <= 1024 && x_rows > 0);
-  KG_CHECK(n > 0 && n % 256 == 0 && k > 0 && k % 128 == 0 && rows > 0 && rows % 128 == 0 && rows <= sf_rows &&
-           k <= lda);
-  KG_CHECK(lda % 16 == 0 && kg_aligned(x, 16) && kg_aligned(w, 16) && kg_aligned(q, 16));
-  KG_CHECK((long long)rows * (n / 2) < (1ll << 31));
-  KG_CHECK(kg_aligned(xsf, 4) && kg_aligned(sfb, 4) && kg_aligned(route_map, 4));
-  KG_CHECK((long long)((k + 511) >> 9) * x_rows * 4 < (1ll << 31) && (long long)((k + 511) >> 9) * n * 4 < (1ll << 31));
-  KG_CHECK((long long)((n / 2 + 511) >> 9) * sf_rows * 4 < (1ll << 31));
-  KgFp8Args p{};
-  p.a = (const u8*)x, p.w = (const u8*)w, p.sfa = (const u32*)xsf, p.sfb = (const u32*)sfb, p.rmap = route_map;
-  p.psum = psum, p.q = (u8*)q, p.qsf = (u8*)sf, p.m = rows, p.n = n, p.k = k, p.rows = rows, p.a_rows = x_rows;
-  p.lda = lda, p.ldc = n, p.sfa_rows = x_rows, p.groups = groups, p.sf_rows = sf_rows;
-  p.m_tiles = (rows + 255) / 256 + groups, p.n_tiles = (n / 2) / 128;
-  const long long total = (long long)p.m_tiles * p.n_tiles;
-  KG_CHECK(total < (1ll << 31) && (long long)x_rows * lda < (1ll << 31) && (long long)n * k < (1ll << 31) &&
-           256ll * lda < (1ll << 31));
-  return kg_fp8_launch_persistent<3>(p, total, (hipStream_t)stream);
-}

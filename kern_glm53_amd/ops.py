@@ -71,14 +71,6 @@ def fp8_gemm_psum_silu_quant(a, w, sfa, sfb, psum, q, sf, *, n: int, k: int, row
          sfa_rows, _ptr(q), _ptr(sf), sf_rows, _stream())
 
 
-def fp8_gemm_psum_gather_silu_quant(x, xsf, x_rows: int, route_map, w, sfb, psum, q, sf, *, n: int, k: int, rows: int,
-                                    lda: int, sf_rows: int, groups: int = EXPERTS):
-    """fp8_gemm_psum_silu_quant reading its A rows through the routing's route_map (row r = x[route_map[r]],
-    scale words xsf[.][route_map[r]]): the gather (source/glm_glue.cu:463-475) folded into the A load."""
-    call("kg_fp8_gemm_psum_gather_silu_quant", _ptr(x), _ptr(xsf), x_rows, _ptr(route_map), _ptr(w), _ptr(sfb),
-         _ptr(psum), groups, n, k, rows, lda, _ptr(q), _ptr(sf), sf_rows, _stream())
-
-
 def bf16_batched(a, b, d, m: int, *, n: int, k: int, rows: int, a_strides, b_strides, d_strides, heads: int = 64):
     """`bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:88-99): D[r][h][:n] = A[r][h][:k] . B[h][:n][:k]^T
     with each operand's byte strides (row, head) as in the reference."""

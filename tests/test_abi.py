@@ -79,13 +79,6 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     # fused: n not a multiple of 256
     ("kg_fp8_gemm_psum_silu_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, 256, 384, 256, 128, 256, 128, FAKE, FAKE, 128,
                                      NULL]),
-    # gathered fused GEMM: no route_map, n % 256, token rows whose byte offsets pass 2^31
-    ("kg_fp8_gemm_psum_gather_silu_quant", [FAKE, FAKE, 16, NULL, FAKE, FAKE, FAKE, 256, 512, 256, 128, 256, FAKE,
-                                            FAKE, 128, NULL]),
-    ("kg_fp8_gemm_psum_gather_silu_quant", [FAKE, FAKE, 16, FAKE, FAKE, FAKE, FAKE, 256, 384, 256, 128, 256, FAKE,
-                                            FAKE, 128, NULL]),
-    ("kg_fp8_gemm_psum_gather_silu_quant", [FAKE, FAKE, 1 << 20, FAKE, FAKE, FAKE, FAKE, 256, 512, 6144, 128, 6144,
-                                            FAKE, FAKE, 128, NULL]),
     # batched: k not a multiple of 64, misaligned stride
     ("kg_bf16_batched", [FAKE, FAKE, FAKE, 16, 512, 100, 16, 64, 40960, 512, 384, 196608, 73728, 1152, NULL]),
     ("kg_bf16_batched", [FAKE, FAKE, FAKE, 16, 512, 192, 16, 64, 40961, 512, 384, 196608, 73728, 1152, NULL]),

@@ -3,9 +3,8 @@
 The kernel fills all 256 VGPRs and 256 AGPRs of a wave.  A value the compiler holds across the tile loop in a
 VGPR then goes to scratch, and every reload carries `s_waitcnt vmcnt(0)`: it waits for all the DMA and stores
 in flight, once or more per tile.  Modes 0 (dense), 1 (grouped) and 2 (grouped with the fused SiLU epilogue),
-the modes the path uses, must compile with no VGPR spills; this test compiles the source to gfx950 assembly
-with the library's own flags and reads the spill counts from the code object's metadata.  (Mode 3, the
-gathered-A variant that is measured but not used, spills by design and is not checked.)"""
+must compile with no VGPR spills; this test compiles the source to gfx950 assembly with the library's own flags
+and reads the spill counts from the code object's metadata."""
 import re
 import subprocess
 
