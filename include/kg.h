@@ -55,6 +55,29 @@ int kg_fp8_gemm_psum_silu_quant(const void* a, const void* w, const void* sfa, c
                                 int groups, int n, int k, int rows, int lda, int sfa_rows, void* q, void* sf,
                                 int sf_rows, void* stream);
 
+/* Weight operand in fragment order, once at load time (a derive step like glm_prep's requant,
+ * source/glm_prep.cu:30-74; no counterpart in the reference, whose DeepGEMM reads row-major weights).
+ * w: e4m3 [rows][k] row-major (kg_requant's output); wf: the same bytes regrouped into blocks of 32 rows x 64
+ * K bytes, block (T, b) at (T k/64 + b) * 2048, byte h*1024 + l*16 + x of a block = w[32T + (l & 31)]
+ * [64b + 32(l >> 5) + 16h + x] (l < 64, h < 2, x < 16): one v_mfma_scale_f32_32x32x64_f8f6f4 operand as the
+ * 64 lanes hold it.  The scale words are unchanged.  Requires rows % 32 == 0, k % 128 == 0, 16-byte aligned
+ * pointers, and wf not overlapping w. */
+int kg_fp8_weight_frag(const void* w, void* wf, long long rows, int k, void* stream);
+
+/* kg_fp8_gemm, kg_fp8_gemm_psum and kg_fp8_gemm_psum_silu_quant with the weights in fragment order
+ * (kg_fp8_weight_frag): the same ops (source/glm_deepgemm.cu:38-41; scripts/glm_ops.py:57-78;
+ * scripts/gen.py:442-443), the same arguments and bit-identical outputs; the weight operand goes from HBM
+ * straight into the MFMA's registers instead of through LDS.  In addition to the row-major variants'
+ * requirements: n % 32 == 0, ldc % 8 == 0 and c 16-byte aligned (dense); n % 512 == 0 (grouped); and
+ * rows * lda, rows * ldc * 2 below 2^31. */
+int kg_fp8_gemm_wf(const void* a, const void* wf, const void* sfa, const void* sfb, void* c, int m, int n, int k,
+                   int rows, int lda, int ldc, int sfa_rows, void* stream);
+int kg_fp8_gemm_psum_wf(const void* a, const void* wf, const void* sfa, const void* sfb, void* c, const int* psum,
+                        int groups, int n, int k, int rows, int lda, int ldc, int sfa_rows, void* stream);
+int kg_fp8_gemm_psum_silu_quant_wf(const void* a, const void* wf, const void* sfa, const void* sfb, const int* psum,
+                                   int groups, int n, int k, int rows, int lda, int sfa_rows, void* q, void* sf,
+                                   int sf_rows, void* stream);
+
 /* bf16 GEMM batched over heads.  Replaces `bf16_batched(n, k, rows, a, b, d)` (scripts/glm_ops.py:88-99;
  * instance source/glm_deepgemm.cu:42-43):  D[r][h][0:n] = bf16(sum_k A[r][h][k] B[h][d][k]), f32
  * accumulation, r < m, h < heads.  Every operand is a byte-strided view: element (r, h, x) of A at

@@ -20,6 +20,10 @@ SIGNATURES = {
     "kg_fp8_gemm": [P, P, P, P, P, I, I, I, I, I, I, I, P],
     "kg_fp8_gemm_psum": [P, P, P, P, P, P, I, I, I, I, I, I, I, P],
     "kg_fp8_gemm_psum_silu_quant": [P, P, P, P, P, I, I, I, I, I, I, P, P, I, P],
+    "kg_fp8_weight_frag": [P, P, LL, I, P],
+    "kg_fp8_gemm_wf": [P, P, P, P, P, I, I, I, I, I, I, I, P],
+    "kg_fp8_gemm_psum_wf": [P, P, P, P, P, P, I, I, I, I, I, I, I, P],
+    "kg_fp8_gemm_psum_silu_quant_wf": [P, P, P, P, P, I, I, I, I, I, I, P, P, I, P],
     "kg_bf16_batched": [P, P, P, I, I, I, I, I, LL, LL, LL, LL, LL, LL, P],
     "kg_mqa_logits": [P, P, P, P, P, P, P, I, I, I, P],
     "kg_gemm_bf16": [P, P, P, I, I, I, I, P],

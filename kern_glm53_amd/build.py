@@ -32,6 +32,7 @@ SOURCES = {
     "kg_norm_rope.hip": ["-ffp-contract=off"],
     "kg_indexer.hip": ["-ffp-contract=off"],
     "kg_fp8_gemm.hip": [],
+    "kg_fp8_wfrag.hip": [],
     "kg_bf16_batched.hip": [],
     "kg_mqa_logits.hip": ["-fno-honor-nans"],
 }

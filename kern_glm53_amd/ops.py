@@ -14,7 +14,8 @@ import torch
 from ._lib import call
 
 __all__ = [
-    "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "bf16_batched", "gemm_bf16", "gemm_f32", "mqa_logits",
+    "fp8_gemm", "fp8_gemm_psum", "fp8_gemm_psum_silu_quant", "fp8_weight_frag", "fp8_gemm_wf", "fp8_gemm_psum_wf",
+    "fp8_gemm_psum_silu_quant_wf", "bf16_batched", "gemm_bf16", "gemm_f32", "mqa_logits",
     "quant",
     "silu_mul_quant", "routing", "moe_psum", "moe_gather", "moe_combine", "router_topk", "requant", "kvb",
     "add_rms_quant", "mla_prep", "q_post", "topk_prefill", "topk_stream", "topk_slots", "idx_gather", "kv_dequant",
@@ -69,6 +70,32 @@ def fp8_gemm_psum_silu_quant(a, w, sfa, sfb, psum, q, sf, *, n: int, k: int, row
     UE8M0 scale words [n/2/512][sf_rows] straight from the accumulators."""
     call("kg_fp8_gemm_psum_silu_quant", _ptr(a), _ptr(w), _ptr(sfa), _ptr(sfb), _ptr(psum), groups, n, k, rows, lda,
          sfa_rows, _ptr(q), _ptr(sf), sf_rows, _stream())
+
+
+def fp8_weight_frag(w, wf, rows: int, k: int):
+    """Load-time derive of the fragment-order weight layout (include/kg.h, kg_fp8_weight_frag): wf holds w's
+    [rows][k] e4m3 bytes as 2 KB blocks of 32 rows x 64 K bytes in MFMA operand order."""
+    call("kg_fp8_weight_frag", _ptr(w), _ptr(wf), rows, k, _stream())
+
+
+def fp8_gemm_wf(a, wf, sfa, sfb, c, m: int, *, n: int, k: int, rows: int, lda: int, ldc: int, sfa_rows: int):
+    """fp8_gemm with the weights in fragment order (fp8_weight_frag); the same outputs."""
+    call("kg_fp8_gemm_wf", _ptr(a), _ptr(wf), _ptr(sfa), _ptr(sfb), _ptr(c), m, n, k, rows, lda, ldc, sfa_rows,
+         _stream())
+
+
+def fp8_gemm_psum_wf(a, wf, sfa, sfb, c, psum, *, n: int, k: int, rows: int, lda: int, ldc: int, sfa_rows: int,
+                     groups: int = EXPERTS):
+    """fp8_gemm_psum with the weights in fragment order (fp8_weight_frag); the same outputs."""
+    call("kg_fp8_gemm_psum_wf", _ptr(a), _ptr(wf), _ptr(sfa), _ptr(sfb), _ptr(c), _ptr(psum), groups, n, k, rows,
+         lda, ldc, sfa_rows, _stream())
+
+
+def fp8_gemm_psum_silu_quant_wf(a, wf, sfa, sfb, psum, q, sf, *, n: int, k: int, rows: int, lda: int,
+                                sfa_rows: int, sf_rows: int, groups: int = EXPERTS):
+    """fp8_gemm_psum_silu_quant with the weights in fragment order (fp8_weight_frag); the same outputs."""
+    call("kg_fp8_gemm_psum_silu_quant_wf", _ptr(a), _ptr(wf), _ptr(sfa), _ptr(sfb), _ptr(psum), groups, n, k, rows,
+         lda, sfa_rows, _ptr(q), _ptr(sf), sf_rows, _stream())
 
 
 def bf16_batched(a, b, d, m: int, *, n: int, k: int, rows: int, a_strides, b_strides, d_strides, heads: int = 64):

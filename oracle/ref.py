@@ -355,6 +355,20 @@ def requant(w8, s, wq, sf, rows, K, group_rows, dst_group_rows=0, dst_row0=0, sf
                       ctypes.c_int(sf_ld if sf_ld is not None else rows), ctypes.c_longlong(sf_group))
 
 
+def weight_frag(w: np.ndarray) -> np.ndarray:
+    """The fragment-order weight layout (include/kg.h, kg_fp8_weight_frag; a load-time regrouping with no
+    counterpart in the reference): w e4m3 [rows][k] -> the same bytes as 2 KB blocks of 32 rows x 64 K bytes,
+    block (T, b) at (T k/64 + b) * 2048, byte h*1024 + l*16 + x = w[32T + (l & 31)][64b + 32(l >> 5) + 16h + x].
+    Pinned in tests/test_oracle.py (a permutation of the bytes; every block the 32 x 64 sub-block it names; each
+    lane's 32 bytes one row's K range, as the fp8 MFMA operand takes it)."""
+    w = np.asarray(w, np.uint8)
+    rows, k = w.shape
+    assert rows % 32 == 0 and k % 64 == 0
+    # [T][r32][b][hi32][h][x] -> [T][b][h][hi32][r32][x]  (lane l = 32 hi32 + r32)
+    v = w.reshape(rows // 32, 32, k // 64, 2, 2, 16)
+    return np.ascontiguousarray(v.transpose(0, 2, 4, 3, 1, 5)).reshape(rows, k)
+
+
 def kvb(w8, s):
     """glm_kvb (source/glm_prep.cu:76-85): bf16 bits kvb [64*448][512], wuk [64][512][192]."""
     w8 = np.ascontiguousarray(w8, dtype=np.uint8)

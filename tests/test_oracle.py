@@ -567,3 +567,32 @@ def test_window_bar_passes_the_model_and_catches_a_scale_byte():
     bad = torch.from_numpy(ref.fp8_gemm_mfma(a, wq, bad_sfa, sfb, M, N, K, K, M))
     ok, rep = ref.check_bf16_gemm(bad.to(torch.bfloat16).float(), ref32, S, K, window=window)
     assert not ok and rep["n_over_window"] > 0
+
+
+def test_weight_frag_layout():
+    """The fragment-order layout (ref.weight_frag) pinned by what it must be, not by its own formula: a byte
+    permutation; block (T, b) holds exactly rows 32T.. x K bytes 64b.. of the row-major matrix; and lane l of
+    a block reads, in its two 16-byte halves (h = 0, 1 at l*16 and 1024 + l*16), the 32 contiguous K bytes
+    [32 (l >> 5), + 32) of row l & 31 -- the fp8 MFMA operand as the row-major kernel gathers it from LDS
+    (chunk 2 (l >> 5) + h of the 64-byte K half)."""
+    rows, k = 96, 256
+    r = np.arange(rows)[:, None]
+    c = np.arange(k)[None, :]
+    ident = (r * k + c).astype(np.int64)                       # a tag per element
+    tag = ident.astype(np.uint32)
+    # the layout moves bytes; carry each element's tag through it as four byte planes
+    planes = [ref.weight_frag(((tag >> (8 * i)) & 0xff).astype(np.uint8)).astype(np.uint32) for i in range(4)]
+    moved = planes[0] | planes[1] << 8 | planes[2] << 16 | planes[3] << 24
+    flat = moved.reshape(-1)
+    assert np.array_equal(np.sort(flat), np.arange(rows * k))          # a permutation
+    blocks = flat.reshape(rows // 32, k // 64, 2048)
+    for T in range(rows // 32):
+        for b in range(k // 64):
+            blk = blocks[T, b]
+            src_r, src_c = blk // k, blk % k
+            assert src_r.min() == 32 * T and src_r.max() == 32 * T + 31
+            assert src_c.min() == 64 * b and src_c.max() == 64 * b + 63
+            for lane in (0, 1, 31, 32, 45, 63):
+                got = np.concatenate([blk[lane * 16:lane * 16 + 16], blk[1024 + lane * 16:1024 + lane * 16 + 16]])
+                want = (32 * T + (lane & 31)) * k + 64 * b + 32 * (lane >> 5) + np.arange(32)
+                assert np.array_equal(got, want), (T, b, lane)
