@@ -5,7 +5,8 @@ normed row to the block's output h, with the gate_up GEMM and `silu_moe` fused i
     topk    router_topk(rl, bias, rs) -> ids, wts                       (kg_router_topk)
     routing FlashInfer tables from ids; psum                            (kg_moe_routing, kg_moe_psum)
     gather  the routed rows of xq / xsf into mq / msf                   (kg_moe_gather)
-    fc1     m-grouped gate_up with the SiLU-mul-quant epilogue -> mq2   (kg_fp8_gemm_psum_silu_quant)
+    fc1     m-grouped gate_up with the SiLU-mul-quant epilogue -> mq2   (kg_fp8_gemm_psum_silu_quant_wf, or
+            (the weights in fragment order, derived at load time)     kg_fp8_gemm_psum_silu_quant without them)
     fc2     m-grouped down -> f2                                        (kg_fp8_gemm_psum)
     shared  gate_up with the SiLU-mul-quant epilogue (one group: rows   (kg_fp8_gemm_psum_silu_quant,
             [0, T)), down on xq -> sh                                    kg_fp8_gemm)
@@ -18,7 +19,9 @@ scale words for `x_rows` rows (the chunk).  Every buffer is allocated once by `M
 nothing, and with T = MoEBuffers.T (the default) every launch of the block is one of this library's kernels.  The routed-row buffers start zeroed: the GEMMs read (and never store) their padding rows.  Weights
 are the reference's operand layouts (glm_requant's output): w13 [256 * 4096][6144] with scale words
 [256 * 12][4096], w2 [256 * 6144][2048] with [256 * 4][6144], the shared expert's w_sgu [4096][6144] /
-[12][4096] and w_sdn [6144][2048] / [4][6144].
+[12][4096] and w_sdn [6144][2048] / [4][6144].  `w13f`, when given, holds w13 in fragment order
+(kern_glm53_amd.ops.fp8_weight_frag, once at load time): fc1 then loads its weight operand straight into the
+MFMA's registers (the same outputs, bit for bit).
 """
 from __future__ import annotations
 
@@ -48,6 +51,7 @@ class MoEWeights:
     sf_sgu: torch.Tensor
     w_sdn: torch.Tensor
     sf_sdn: torch.Tensor
+    w13f: torch.Tensor | None = None     # w13 in fragment order (optional)
 
 
 class MoEBuffers:
@@ -95,8 +99,9 @@ def moe_block(xn, xq, xsf, w: MoEWeights, b: MoEBuffers, h, T: int | None = None
     mark("psum")
     ops.moe_gather(xq, xsf, b.x_rows, b.exp2perm, b.mq, b.msf, b.mcap, T=T)
     mark("gather")
-    ops.fp8_gemm_psum_silu_quant(b.mq, w.w13, b.msf, w.sf13, b.psum, b.mq2, b.msf2, n=2 * INTER, k=H, rows=b.mcap,
-                                 lda=H, sfa_rows=b.mcap, sf_rows=b.mcap)
+    fc1 = ops.fp8_gemm_psum_silu_quant if w.w13f is None else ops.fp8_gemm_psum_silu_quant_wf
+    fc1(b.mq, w.w13 if w.w13f is None else w.w13f, b.msf, w.sf13, b.psum, b.mq2, b.msf2, n=2 * INTER, k=H, rows=b.mcap,
+        lda=H, sfa_rows=b.mcap, sf_rows=b.mcap)
     mark("fc1_silu_quant")
     ops.fp8_gemm_psum(b.mq2, w.w2, b.msf2, w.sf2, b.f2, b.psum, n=H, k=INTER, rows=b.mcap, lda=INTER, ldc=H,
                       sfa_rows=b.mcap)
