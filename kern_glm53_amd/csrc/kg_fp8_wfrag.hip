@@ -361,15 +361,22 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
     asm volatile("" ::: "memory");                                                                        \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
   } while (0)
-  // The stage barrier.  The loads issued after this wave's last DMA instruction of stage s + 1 (slot 31 of
-  // stage s - 1) and before the barrier are the 8 K-half-1 weight loads of slots 0..7, the 4 DMA instructions
-  // of slots 9..15 and the 7 K-half-0 weight loads of slots 16..22 (on PH 2 the next word group too): 19.
-  // Loads complete in issue order, so with that DMA outstanding at least 20 operations are, and vmcnt(18)
-  // (one of margin) cannot pass; stores in flight (an epilogue's) can complete in any order but only add to
-  // the count, so they make the wait longer, never too short.  Scheduling barriers on both sides keep
-  // slot 22's load and MFMA from moving across it (the machine scheduler moves instructions across an
-  // inline asm statement, which would shrink the count).
-#define KG_WBARRIER() asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory")
+  // The stage barrier of stage s.  Vector-memory loads complete in issue order, so the ring issues them in
+  // the order they are needed (the weight fragments of a K half by their first MFMA, a stage's DMA by the
+  // barrier that publishes it): a barrier then never waits for a load needed later than its DMA.  The loads
+  // issued after this wave's last DMA instruction of stage s + 1 (slot 15 of stage s - 1) and before the
+  // barrier are the K-half-0 weight loads of slots 16..23 of stage s - 1, and in stage s the K-half-1 loads of
+  // slots 0..7, the DMA of slots 8..15 and the K-half-0 loads of slots 16..22: 31, plus on PH 3 the word
+  // group that stage s - 1 (PH 2) issued at slot 16.  With that DMA outstanding at least 32 (40) operations
+  // are, and vmcnt(30) (vmcnt(38)), one of margin, cannot pass; stores in flight (an epilogue's) can complete
+  // in any order but only add to the count, so they make the wait longer, never too short.  Scheduling
+  // barriers on both sides keep slot 22's load and MFMA from moving across it (the machine scheduler moves
+  // instructions across an inline asm statement, which would shrink the count).
+#define KG_WBARRIER(PH)                                                                                    \
+  do {                                                                                                    \
+    if constexpr ((PH) == 3) asm volatile("s_waitcnt vmcnt(38) lgkmcnt(0)\n\ts_barrier" ::: "memory");    \
+    else asm volatile("s_waitcnt vmcnt(30) lgkmcnt(0)\n\ts_barrier" ::: "memory");                        \
+  } while (0)
   // MFMA of slot (K half KH, activation tile N, weight tile O) in a stage with scale byte PH
 #define KG_MFMA(PH, KH, N, O)                                                                              \
   acc[O][N] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[(PH) & 1][KH][O], af[((KH) * 4 + (N)) & 3], \
@@ -382,17 +389,18 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
   } while (0)
   // One stage s (PH = its index in the group of four = its buffer = the byte of the scale words; the weight
   // set is PH & 1): 32 MFMA slots t = 16 kh + 4 n + o (K half kh, activation tile n, weight tile o).  After
-  // slot t at most one vector-memory instruction (1 KB), so that the queue never takes a burst:
+  // slot t at most one vector-memory instruction (1 KB), so that the queue never takes a burst, in the order
+  // the loads are needed:
   //   * t = 4 q: the LDS read of activation fragment q + 2 (q + 2 >= 8: the next stage's, from its buffer);
   //   * t = 0..7: half t & 1 of stage s + 1's K-half-1 weight fragment t >> 1 (source D1 / K1) into the other
   //     set, whose K-half-1 fragments of stage s - 1 retired in slots 28..31;
-  //   * t = 9, 11, 13, 15 and 25, 27, 29, 31: DMA instructions 0..7 of stage s + 2 (source DA / TA / KA) into
-  //     buffer (PH + 2) & 3, free since the barrier of stage s - 2; on PH 2 the next word group at t = 10..13;
+  //   * t = 8..15: DMA instruction t - 8 of stage s + 2 (source DA / TA / KA) into buffer (PH + 2) & 3, free
+  //     since the barrier of stage s - 2;
+  //   * on PH 2, the next word group at t = 16;
   //   * t = 16..23: half t & 1 of stage s + 2's K-half-0 weight fragment (t - 16) >> 1 (source D2 / K2) into
   //     this set, whose K-half-0 fragments retired in slots 12..15;
   //   * the barrier after slot 22 (the last read of this stage's buffer is slot 20's).
-  // Every weight fragment is loaded about 1.5 stages before its MFMA, every DMA 0.7 to 1.2 stages before
-  // the barrier that publishes it.
+  // Every load goes out 1.2 to 1.5 stages before it is needed.
 #define KG_WSTAGE(PH, DA, TA, KA, D2, K2, D1, K1)                                                          \
   do {                                                                                                    \
     u8* const cur_ = (PH) == 0 ? ab0 : (PH) == 1 ? ab1 : (PH) == 2 ? ab2 : ab3;                           \
@@ -407,16 +415,17 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
         else af[r_ & 3] = KG_AFRAG(nxt_, 0, r_ - 8);                                                      \
       }                                                                                                   \
       if (t_ < 8) wset(wf[((PH) & 1) ^ 1][1][t_ >> 1], t_ & 1, wload(D1, K1, t_ >> 1, 1, t_ & 1));        \
+      if (t_ >= 8 && t_ < 16) dma_a(dst_, DA, TA, KA, t_ - 8);                                              \
+      if (t_ == 16 && (PH) == 2) {                                                                         \
+        KG_ISSUE_ORDER();                                                                                 \
+        words(wt, wkg, wa[1], wb[1]);                                                                     \
+        KG_ISSUE_ORDER();                                                                                 \
+      }                                                                                                   \
       if (t_ >= 16 && t_ < 24) wset(wf[(PH) & 1][0][(t_ - 16) >> 1], t_ & 1, wload(D2, K2, (t_ - 16) >> 1, 0, t_ & 1)); \
       if (t_ == 22) {                                                                                      \
         __builtin_amdgcn_sched_barrier(0);                                                                \
-        KG_WBARRIER();                                                                                    \
+        KG_WBARRIER(PH);                                                                                  \
         __builtin_amdgcn_sched_barrier(0);                                                                \
-      }                                                                                                   \
-      if ((t_ & 1) && ((t_ >= 9 && t_ < 16) || t_ >= 25)) dma_a(dst_, DA, TA, KA, (t_ < 16 ? (t_ - 9) : (t_ - 17)) >> 1); \
-      if (t_ == 10 && (PH) == 2) {                                                                         \
-        KG_ISSUE_ORDER();                                                                                 \
-        words(wt, wkg, wa[1], wb[1]);                                                                     \
       }                                                                                                   \
       KG_ISSUE_ORDER();                                                                                   \
     }                                                                                                     \
