@@ -113,6 +113,19 @@ KG_DEV float kg_silu_mul_bf16(float g, float u) {
   return kg_bf16_to_f32(kg_f32_to_bf16(kg_silu_f32(g) * u));
 }
 
+// The fused epilogue's form of it for two outputs straight from f32 accumulators: the gate and up sums
+// rounded to bf16 as the GEMM's bf16 output would hold them, then SiLU(g) * u rounded to bf16 and back.
+// The same roundings as kg_silu_mul_bf16 of kg_f32_to_bf16 values, with each pair of them done by one
+// v_cvt_pk_bf16_f32 (gate with up, then the two products).
+KG_DEV void kg_silu_mul_acc_bf16x2(float g0, float u0, float g1, float u1, float& r0, float& r1) {
+  const u32 p0 = kg_pack_bf16x2(g0, u0), p1 = kg_pack_bf16x2(g1, u1);
+  const float s0 = kg_silu_f32(kg_u2f(p0 << 16)) * kg_u2f(p0 & 0xffff0000u);
+  const float s1 = kg_silu_f32(kg_u2f(p1 << 16)) * kg_u2f(p1 & 0xffff0000u);
+  const u32 q = kg_pack_bf16x2(s0, s1);
+  r0 = kg_u2f(q << 16);
+  r1 = kg_u2f(q & 0xffff0000u);
+}
+
 // This lane's id within the wave (v_mbcnt), formed where it is used: the count starts from a zero that an
 // empty volatile asm produces at the call, so neither the v_mbcnt pair nor the address arithmetic built on
 // it can be hoisted out of a loop into a register held across it (with every register taken, such a value

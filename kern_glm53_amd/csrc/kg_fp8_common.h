@@ -224,11 +224,12 @@ KG_DEV void kg_fp8_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stag
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float v = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
-                                         kg_bf16_to_f32(kg_f32_to_bf16(acc[i + 2][j][r])));
-        acc[i][j][r] = v;                        // the product overwrites the gate accumulator
-        am = fmaxf(am, fabsf(v));
+      for (int r = 0; r < 16; r += 2) {
+        float v0, v1;
+        kg_silu_mul_acc_bf16x2(acc[i][j][r], acc[i + 2][j][r], acc[i][j][r + 1], acc[i + 2][j][r + 1], v0, v1);
+        acc[i][j][r] = v0;                       // the product overwrites the gate accumulator
+        acc[i][j][r + 1] = v1;
+        am = fmaxf(fmaxf(am, fabsf(v0)), fabsf(v1));
       }
     // the other half-wave's value (lane ^ 32), addressed from this call's lane id: __shfl_xor's own lane id
     // would be formed once, before the tile loop, and held (spilled) across it

@@ -177,10 +177,10 @@ KG_DEV void kg_wf_epilogue_silu(const KgFp8Args& p, v16f (&acc)[4][4], u8* stage
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        v[i][r] = kg_silu_mul_bf16(kg_bf16_to_f32(kg_f32_to_bf16(acc[i][j][r])),
-                                   kg_bf16_to_f32(kg_f32_to_bf16(acc[i + 2][j][r])));
-        am = fmaxf(am, fabsf(v[i][r]));
+      for (int r = 0; r < 16; r += 2) {
+        kg_silu_mul_acc_bf16x2(acc[i][j][r], acc[i + 2][j][r], acc[i][j][r + 1], acc[i + 2][j][r + 1], v[i][r],
+                               v[i][r + 1]);
+        am = fmaxf(fmaxf(am, fabsf(v[i][r])), fabsf(v[i][r + 1]));
       }
     am = fmaxf(am, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, am))));
     const int sr = srow0 + j * 32;
