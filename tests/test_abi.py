@@ -51,6 +51,8 @@ NULL = None
     ("kg_add_rms_quant", [NULL, NULL, NULL, NULL, NULL, NULL, 16, 16, NULL]),
     ("kg_mla_prep", [NULL, 2752, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 16, 16, 64, 64,
                      NULL]),
+    ("kg_fp8_weight_frag", [NULL, NULL, 64, 128, NULL]),
+    ("kg_fp8_gemm_psum_wf", [NULL, NULL, NULL, NULL, NULL, NULL, 256, 512, 256, 128, 256, 512, 128, NULL]),
     ("kg_q_post", [NULL, 20480, NULL, NULL, NULL, NULL, NULL, NULL, 1, 16, 64, NULL]),
 ])
 def test_null_pointers_rejected(name, args):
@@ -79,6 +81,15 @@ FAKE = ctypes.c_void_p(1 << 40)   # never dereferenced: validation fails first
     # fused: n not a multiple of 256
     ("kg_fp8_gemm_psum_silu_quant", [FAKE, FAKE, FAKE, FAKE, FAKE, 256, 384, 256, 128, 256, 128, FAKE, FAKE, 128,
                                      NULL]),
+    # fragment order: rows % 32, k % 128, in place (the output overlaps the input)
+    ("kg_fp8_weight_frag", [FAKE, ctypes.c_void_p((1 << 40) + (1 << 30)), 48, 128, NULL]),
+    ("kg_fp8_weight_frag", [FAKE, ctypes.c_void_p((1 << 40) + (1 << 30)), 64, 100, NULL]),
+    ("kg_fp8_weight_frag", [FAKE, ctypes.c_void_p((1 << 40) + 4096), 64, 128, NULL]),
+    # dense over fragment-order weights: n % 32; grouped and fused: n % 512 (column tiles in pairs)
+    ("kg_fp8_gemm_wf", [FAKE, FAKE, FAKE, FAKE, FAKE, 16, 48, 128, 16, 128, 128, 16, NULL]),
+    ("kg_fp8_gemm_psum_wf", [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 256, 128, 256, 256, 128, NULL]),
+    ("kg_fp8_gemm_psum_silu_quant_wf", [FAKE, FAKE, FAKE, FAKE, FAKE, 256, 256, 256, 128, 256, 128, FAKE, FAKE,
+                                        128, NULL]),
     # batched: k not a multiple of 64, misaligned stride
     ("kg_bf16_batched", [FAKE, FAKE, FAKE, 16, 512, 100, 16, 64, 40960, 512, 384, 196608, 73728, 1152, NULL]),
     ("kg_bf16_batched", [FAKE, FAKE, FAKE, 16, 512, 192, 16, 64, 40961, 512, 384, 196608, 73728, 1152, NULL]),
