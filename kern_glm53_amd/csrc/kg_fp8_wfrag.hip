@@ -4,9 +4,10 @@
 // weight operand loaded from HBM straight into VGPRs instead of through LDS.
 //
 // Why.  The row-major kernel moves both 256 x 128 operand tiles of a stage through LDS: 64 KB of DMA writes
-// and 128 KB of fragment reads per CU per 2048 MFMA cycles, which the LDS cannot serve alongside the matrix
-// pipe.  Here only the activation tile goes through LDS (32 KB written, 64 KB read per stage): each wave
-// loads the fragments of its own 128 weight rows as they sit in the MFMA's operand registers.
+// and 128 KB of fragment reads per CU per stage.  Here only the activation tile goes through LDS (32 KB
+// written, 64 KB read per stage): each wave loads the fragments of its own 128 weight rows as they sit in
+// the MFMA's operand registers, and an expert's tail of at most 128 rows can cover two column tiles.  It
+// pays where the weights stream from HBM (the MoE gate_up); on dense shapes the row-major kernel is as fast.
 //
 // Fragment order (kg_fp8_weight_frag, once at load time).  The weight matrix [rows][k] (rows % 32 == 0) is
 // cut into blocks of 32 rows x 64 K bytes; block (T, b) (row tile T, K block b) is 2 KB at
@@ -21,19 +22,21 @@
 //     weight rows wn * 128 .. (4 MFMA tiles, operand A); the 256 accumulators stay in AGPRs.
 //   * K advances 128 (one scale block) per stage.  Activations: 4 LDS buffers of 32 KB (the row-major
 //     kernel's swizzled 128-byte rows, filled by buffer_load ... lds), stage s in buffer s & 3, its DMA
-//     issued two stages ahead.  Weights: two register sets of 8 fragments (64 VGPRs each), stage s in set
-//     s & 1, each fragment reloaded for stage s + 2 right after its last MFMA in stage s.
+//     issued during stage s - 2.  Weights: two register sets of 8 fragments (64 VGPRs each), stage s in set
+//     s & 1; each fragment is reloaded, for the next stage that uses its set, soon after its last MFMA.
 //   * MFMA order in a stage: slot t = 16 kh + 4 n + o (K half kh, activation tile n, weight tile o); the
-//     activation fragment of slot group q = t / 4 is read from LDS two groups ahead (a ring of 4).
+//     activation fragment of slot group q = t / 4 is read from LDS two groups ahead (a ring of 4).  After each
+//     slot at most one 1 KB vector-memory instruction: K-half-1 weights of stage s + 1 (slots 0..7), the DMA
+//     of stage s + 2 (8..15), K-half-0 weights of stage s + 2 (16..23).
 //   * One barrier per stage, after slot 22: this wave's DMA of stage s + 1 has landed (a vmcnt that counts
 //     only the loads issued after it), its reads of stage s's buffer are done, so stage s + 1 is published
-//     and the buffer of stage s is free.  Slots 23..30 issue the DMA of stage s + 2 into buffer (s + 2) & 3,
-//     free since the barrier of stage s - 2.
-//   * Tiles of at most 128 rows (an expert's tail) run 128 x 256 with 16 MFMAs per stage (n < 2), the same
-//     loads, the barrier after slot 6 and the DMA in slots 7..14.
-//   * The ring runs across tiles: a tile's last two stages load the next tile's stages 0 and 1; the
-//     epilogue (the row-major kernel's, staged through buffer 3, which no DMA fills before the next tile's
-//     stage 1) runs with them in flight.
+//     and the buffer of stage s is free for the DMA of stage s + 4.
+//   * An expert's tail of at most 128 rows runs as one tile over two column tiles: the waves with wm = 0
+//     take column tile nt, those with wm = 1 column tile nt + 1, all over the same 128 rows.  Every tile runs
+//     the same 32 MFMAs per wave and stage, so one schedule (and one register allocation) serves all.
+//   * The ring runs across tiles: a tile's last two stages load the next tile's stages 0 and 1 (its stage 1
+//     K-half-0 weights after the epilogue); the epilogue (staged through buffer 3, which no DMA fills before
+//     the next tile's stage 1) runs with them in flight.
 #include "kg_fp8_common.h"
 #include "kg_host.h"
 
@@ -463,8 +466,9 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
   wnull.r0 = wnull.r2 = 0;
 
   for (;;) {
-    // stage 1's K-half-0 weight fragments (stage 0 and stage 1's K half 1 were loaded by the previous tile's
-    // last stages; these were deferred past its epilogue, and the barrier counts only grow by them)
+    // stage 1's K-half-0 weight fragments (stage 0's were loaded by the previous tile's last two stages, and
+    // stage 1's K half 1 goes out in stage 0 as in every stage; these were deferred past the epilogue, and the
+    // barrier counts only grow by them)
 #pragma unroll
     for (int o = 0; o < 4; ++o)
 #pragma unroll
@@ -472,7 +476,7 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
     KG_ISSUE_ORDER();
     const int aoff = cur.tail ? 0 : wm * 128 * 128;
     // stage 0's first two activation fragments (buffer 0 holds it, published by the last barrier; read here
-    // because the previous tile may have been of the other kind)
+    // because the row base depends on the tile's kind)
     af[0] = KG_AFRAG(ab0, 0, 0);
     af[1] = KG_AFRAG(ab0, 0, 1);
 #pragma unroll
