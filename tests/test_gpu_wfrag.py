@@ -7,7 +7,7 @@ feed the MFMA the same operands in the same order; the row-major kernels are pin
 test_gpu_gemm.py, and the dense case here is also held to the oracle's bar and its fp8-MFMA model directly.
 The grouped cases cover expert sizes that make every tile kind: empty experts, tails of 1..128 rows (run as
 column-pair tiles), tails of 129..255 rows (full tiles with masked rows), several full row tiles, one expert
-with tens of row tiles, and the bench's 16384-token Zipf routing at full size."""
+with tens of row tiles, and the bench's 16384-token Zipf routing at full size; seeded random dense and grouped shapes on top."""
 import numpy as np
 import pytest
 import torch
@@ -161,3 +161,59 @@ def test_moe_wf_full_size():
     c1 = filled((rows, H), SENTINEL, torch.int16)
     ops.fp8_gemm_psum_wf(q2, frag(wd), sf2, sfd, c1, dp, n=H, k=INTER, rows=rows, lda=INTER, ldc=H, sfa_rows=rows)
     assert torch.equal(c0, c1)
+
+
+def random_dense_shapes():
+    rng = np.random.default_rng(4242)
+    out = []
+    for i in range(10):
+        M = int(rng.integers(1, 5000))
+        N = 32 * int(rng.integers(1, 160))
+        K = 128 * int(rng.integers(1, 25))
+        lda = K + 16 * int(rng.integers(0, 4))
+        ldc = (N + 7) // 8 * 8 + 8 * int(rng.integers(0, 3))
+        rows = M + int(rng.integers(0, 40))
+        out.append((M, N, K, rows, lda, ldc, rows + int(rng.integers(0, 9))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,rows,lda,ldc,sfa_rows", random_dense_shapes())
+def test_fp8_gemm_wf_random(M, N, K, rows, lda, ldc, sfa_rows):
+    """Seeded random dense shapes (tails in M and N, odd K-block counts, padded strides): bit-identity with
+    kg_fp8_gemm on every byte of C, the untouched ones included."""
+    print(f"dense wf random {M}x{N}x{K} rows={rows} lda={lda} ldc={ldc} sfa_rows={sfa_rows}", flush=True)
+    a, sfa = quant_act(M, K, rows, lda, sfa_rows, seed=M + 7 * N + K)
+    w, sfb = quant_weight(N, K, seed=3 * N + K)
+    da, dw, dsfa, dsfb = d(a), d(w), d(sfa), d(sfb)
+    c0 = filled((rows, ldc), SENTINEL, torch.int16)
+    ops.fp8_gemm(da, dw, dsfa, dsfb, c0, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
+    c1 = filled((rows, ldc), SENTINEL, torch.int16)
+    ops.fp8_gemm_wf(da, frag(dw), dsfa, dsfb, c1, M, n=N, k=K, rows=rows, lda=lda, ldc=ldc, sfa_rows=sfa_rows)
+    assert np.array_equal(h(c0, np.uint16), h(c1, np.uint16))
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_fp8_gemm_grouped_wf_random(seed):
+    """Seeded random grouped shapes (expert counts with empty experts, 1, 7 or 256 groups, K of 1-8 blocks):
+    the grouped and the fused fragment-order GEMMs equal their row-major counterparts on every byte."""
+    rng = np.random.default_rng(500 + seed)
+    groups = int(rng.choice([1, 7, 256]))
+    n, k = int(rng.choice([512, 1024])), 128 * int(rng.integers(1, 9))
+    counts = np.where(rng.random(groups) < 0.75, rng.integers(1, 900, groups), 0).astype(np.int32)
+    print(f"grouped wf random seed={seed}: groups {groups}, n {n}, k {k}", flush=True)
+    psum, rows, a, w, sfa, sfb = grouped(counts, n, k, seed=60 + seed, groups=groups)
+    dp, wf = d(psum), frag(w)
+    c0 = filled((rows, n), SENTINEL, torch.int16)
+    ops.fp8_gemm_psum(a, w, sfa, sfb, c0, dp, n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows, groups=groups)
+    c1 = filled((rows, n), SENTINEL, torch.int16)
+    ops.fp8_gemm_psum_wf(a, wf, sfa, sfb, c1, dp, n=n, k=k, rows=rows, lda=k, ldc=n, sfa_rows=rows, groups=groups)
+    assert np.array_equal(h(c0, np.uint16), h(c1, np.uint16))
+    I = n // 2
+    outs = []
+    for fn, wt in ((ops.fp8_gemm_psum_silu_quant, w), (ops.fp8_gemm_psum_silu_quant_wf, wf)):
+        q = filled((rows, I), 0x5c)
+        sf = filled((ref.sf_words(I) * rows * 4,), 0x5d)
+        fn(a, wt, sfa, sfb, dp, q, sf, n=n, k=k, rows=rows, lda=k, sfa_rows=rows, sf_rows=rows, groups=groups)
+        outs.append((h(q, np.uint8), h(sf, np.uint8)))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
