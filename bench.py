@@ -6,7 +6,7 @@ One step = the fp8 GEMMs of one GLM-5.3 prefill chunk of M = 16384 rows at the r
   * dense  q_a/kv_a  (N=2624, ldc 2752, K=6144), q_b (N=16384, ldc 20480, K=2048), o_proj (N=6144, K=16384);
   * MoE    gate_up   m-grouped psum GEMM over 256 experts, N=4096, K=6144, with the SiLU-mul + e4m3 requant
            epilogue fused (writes the down-proj's operand), and down N=6144, K=2048, on the routing of 16384
-           tokens x top-8 drawn from a Zipf(1.1) expert popularity.  gate_up reads its weights in fragment order
+           tokens x top-8 drawn from a Zipf(1.1) expert popularity.  Both read their weights in fragment order
            (kg_fp8_weight_frag, a load-time derive like the reference's glm_prep requant, outside the timing).
 value = algorithmic FLOPs of the step (2 M N K dense, 2 R N K over the R = 131072 routed rows for the MoE,
 padding excluded) / step time.  Operands are synthetic (seeded), generated and quantized on the GPU by the
@@ -124,6 +124,9 @@ def prepare(dev):
     moe["w2"] = torch.empty(EXPERTS * H, INTER, dtype=torch.uint8, device=dev)
     moe["sf2"] = torch.empty(EXPERTS * sfw(INTER) * H * 4, dtype=torch.uint8, device=dev)
     requant_into(moe["w2"], moe["sf2"], EXPERTS * H, INTER, H, H, H, sfw(INTER) * H, 600, chunk_groups=16)
+    # down's weights in fragment order (load time)
+    moe["w2f"] = torch.empty_like(moe["w2"])
+    ops.fp8_weight_frag(moe["w2"], moe["w2f"], EXPERTS * H, INTER)
     moe["mq2"] = torch.zeros(mcap, INTER, dtype=torch.uint8, device=dev)
     moe["msf2"] = torch.zeros(sfw(INTER) * mcap * 4, dtype=torch.uint8, device=dev)
     moe["f2"] = torch.zeros(mcap, H, dtype=torch.bfloat16, device=dev)
@@ -160,8 +163,8 @@ def launches(data):
                                                         m["msf2"], n=2 * INTER, k=H, rows=mcap, lda=H, sfa_rows=mcap,
                                                         sf_rows=mcap)))
     out.append(("moe_down", 2.0 * R * H * INTER,
-                lambda: ops.fp8_gemm_psum(m["mq2"], m["w2"], m["msf2"], m["sf2"], m["f2"], m["psum"], n=H, k=INTER,
-                                          rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap)))
+                lambda: ops.fp8_gemm_psum_wf(m["mq2"], m["w2f"], m["msf2"], m["sf2"], m["f2"], m["psum"], n=H,
+                                             k=INTER, rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap)))
     return out
 
 
@@ -253,7 +256,8 @@ def moe_block_measure(data, dev, stream, iters=3):
         sw[name] = (wq, sf)
     W = moe.MoEWeights((torch.randn(EXPERTS, H, generator=g, device=dev) * 0.02).to(torch.bfloat16),
                        -0.25 * torch.log1p(rank), torch.tensor([2.5], dtype=torch.bfloat16, device=dev),
-                       m["w13"], m["sf13"], m["w2"], m["sf2"], *sw["sgu"], *sw["sdn"], w13f=m["w13f"])
+                       m["w13"], m["sf13"], m["w2"], m["sf2"], *sw["sgu"], *sw["sdn"], w13f=m["w13f"],
+                       w2f=m["w2f"])
     B = moe.MoEBuffers(M, M, dev)
     out = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
     moe.moe_block(xn, xq, xsf, W, B, out)
@@ -366,8 +370,8 @@ def aux_launches(aux):
 
 def skinny_launches(data, dev):
     """The MoE GEMMs on psum plans of uniformly skinny experts: each of the 256 experts owns r rows, r = 100 (one
-    128-row block: a tail, run over pairs of column tiles by gate_up's fragment-order kernel and as half tiles by
-    the down GEMM) or r = 228 (two blocks: one 256-row tile).  Every launch streams all the experts'
+    128-row block: a tail, run over pairs of column tiles by the fragment-order kernel) or r = 228 (two blocks:
+    one 256-row tile).  Every launch streams all the experts'
     weights (6.4 GB gate_up, 3.2 GB down) for little work per byte: the regime of a real routing's
     low-occupancy experts.  (name, launch, algorithmic flops, algorithmic HBM bytes, expert tiles)."""
     from kern_glm53_amd import ops
@@ -388,10 +392,10 @@ def skinny_launches(data, dev):
                     EXPERTS * 2 * INTER * H + R * H + R * INTER + EXPERTS * 2 * INTER * H // 16384,
                     EXPERTS * (16 if r > 128 else 8)))
         out.append((f"down_r{r}",
-                    lambda psum=psum: ops.fp8_gemm_psum(m["mq2"], m["w2"], m["msf2"], m["sf2"], m["f2"], psum, n=H,
-                                                        k=INTER, rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap),
+                    lambda psum=psum: ops.fp8_gemm_psum_wf(m["mq2"], m["w2f"], m["msf2"], m["sf2"], m["f2"], psum,
+                                                           n=H, k=INTER, rows=mcap, lda=INTER, ldc=H, sfa_rows=mcap),
                     2.0 * R * H * INTER, EXPERTS * H * INTER + R * INTER + R * H * 2 + EXPERTS * H * INTER // 16384,
-                    EXPERTS * 24))
+                    EXPERTS * (24 if r > 128 else 12)))
     return out
 
 

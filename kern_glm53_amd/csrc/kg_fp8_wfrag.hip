@@ -323,7 +323,12 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
   // (row tile, 2 ko / 128 + kh), bytes h * 1024 ... Past K (the padded stages) the offset is KG_OOB: zeros.
   auto wload = [&](const KgWSrc& d, int ko, int o, int kh, int h) -> v4u {
     const int row = (o < 2 ? d.r0 : d.r2) + (o & 1) * 32 * p.k;
-    const unsigned v = l16 + (ko < p.k ? (unsigned)row : KG_OOB) + (unsigned)(kh * 2048 + h * 1024);
+    // mode 1: the lane term passes through an empty asm statement, so that the four lane + half offsets are
+    // formed here rather than held in registers across the tile loop (spilled, their reloads wait for every
+    // load); modes 0 and 2 allocate better without it
+    unsigned lb = l16;
+    if constexpr (MODE == 1) asm volatile("" : "+v"(lb));
+    const unsigned v = lb + (ko < p.k ? (unsigned)row : KG_OOB) + (unsigned)(kh * 2048 + h * 1024);
     return __builtin_amdgcn_raw_buffer_load_b128(d.rw, v, (unsigned)ko * 32u, 0);
   };
   auto wset = [](v8i& f, int h, v4u x) {
@@ -380,11 +385,13 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
     if constexpr ((PH) == 3) asm volatile("s_waitcnt vmcnt(38) lgkmcnt(0)\n\ts_barrier" ::: "memory");    \
     else asm volatile("s_waitcnt vmcnt(30) lgkmcnt(0)\n\ts_barrier" ::: "memory");                        \
   } while (0)
-  // MFMA of slot (K half KH, activation tile N, weight tile O) in a stage with scale byte PH
-#define KG_MFMA(PH, KH, N, O)                                                                              \
+  // MFMA of slot (K half KH, activation tile N, weight tile O) in a stage with scale byte PH; Z: the tile's
+  // first K step, whose sums start from zero (an inline 0 in place of the accumulator, so the tile needs no
+  // 256 accumulator writes to clear them)
+#define KG_MFMA(PH, KH, N, O, Z)                                                                           \
   acc[O][N] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[(PH) & 1][KH][O], af[((KH) * 4 + (N)) & 3], \
-                                                              acc[O][N], 0, 0, (PH), (int)wb[0][O], (PH), \
-                                                              (int)wa[0][N])
+                                                              (Z) ? v16f{} : acc[O][N], 0, 0, (PH),        \
+                                                              (int)wb[0][O], (PH), (int)wa[0][N])
 #define KG_AREAD(R, CUR, NXT)                                                                              \
   do {                                                                                                    \
     if constexpr ((R) < 8) af[(R) & 3] = KG_AFRAG(CUR, (R) >> 2, (R) & 3);                                 \
@@ -404,14 +411,14 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
   //     this set, whose K-half-0 fragments retired in slots 12..15;
   //   * the barrier after slot 22 (the last read of this stage's buffer is slot 20's).
   // Every load goes out 1.2 to 1.5 stages before it is needed.
-#define KG_WSTAGE(PH, DA, TA, KA, D2, K2, D1, K1)                                                          \
+#define KG_WSTAGE(PH, DA, TA, KA, D2, K2, D1, K1, Z)                                                       \
   do {                                                                                                    \
     u8* const cur_ = (PH) == 0 ? ab0 : (PH) == 1 ? ab1 : (PH) == 2 ? ab2 : ab3;                           \
     u8* const nxt_ = (PH) == 0 ? ab1 : (PH) == 1 ? ab2 : (PH) == 2 ? ab3 : ab0;                           \
     u8* const dst_ = (PH) == 0 ? ab2 : (PH) == 1 ? ab3 : (PH) == 2 ? ab0 : ab1;                           \
     __builtin_amdgcn_sched_barrier(0);                                                                    \
     _Pragma("unroll") for (int t_ = 0; t_ < 32; ++t_) {                                                    \
-      KG_MFMA(PH, t_ >> 4, (t_ >> 2) & 3, t_ & 3);                                                        \
+      KG_MFMA(PH, t_ >> 4, (t_ >> 2) & 3, t_ & 3, (Z) && t_ < 16);                                        \
       if ((t_ & 3) == 0) {                                                                                 \
         const int r_ = (t_ >> 2) + 2;                                                                     \
         if (r_ < 8) af[r_ & 3] = KG_AFRAG(cur_, r_ >> 2, r_ & 3);                                          \
@@ -479,41 +486,52 @@ __global__ __launch_bounds__(256, 1) void kg_fp8_gemm_wfrag(const KgFp8Args p) {
     // because the row base depends on the tile's kind)
     af[0] = KG_AFRAG(ab0, 0, 0);
     af[1] = KG_AFRAG(ab0, 0, 1);
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     // Per group of four stages: scale bytes of blocks at or past K get the unit exponent 127; in the last
-    // group, stages 2 and 3 load the next tile's stages 0 and 1 (and the next tile's first word group).
-    for (int ks = 0; ks < KS; ks += 4) {
-      const int live_b = KB - ks;
+    // group, stages 2 and 3 load the next tile's stages 0 and 1 (and the next tile's first word group).  In
+    // mode 1 the first group is peeled: its stage 0's K-half-0 MFMAs start the sums from zero (the MoE down
+    // GEMM 3.5% faster).
+#define KG_WGROUP(Z)                                                                                       \
+  do {                                                                                                    \
+    const int live_b = KB - ks;                                                                           \
+    {                                                                                                     \
+      const u32 keep = live_b >= 4 ? 0xffffffffu : live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));  \
+      const u32 unit = 0x7f7f7f7fu & ~keep;                                                               \
+      _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | unit;                  \
+      _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | unit;                  \
+    }                                                                                                     \
+    const bool lastg = ks + 4 >= KS;                                                                      \
+    const KgWTile wt = lastg ? nxt : cur;                                                                 \
+    const int kn = lastg ? 0 : (ks + 4) * 128, wkg = lastg ? 0 : (ks >> 2) + 1;                           \
+    const KgWSrc wsx = lastg ? wsn : wsc;                                                                 \
+    const unsigned asx = lastg ? asn : asc;                                                               \
+    const int tsx = lastg ? nxt.tail : cur.tail;                                                          \
+    const int k0 = ks * 128;                                                                              \
+    KG_WSTAGE(0, asc, cur.tail, k0 + 256, wsc, k0 + 256, wsc, k0 + 128, Z);                               \
+    KG_WSTAGE(1, asc, cur.tail, k0 + 384, wsc, k0 + 384, wsc, k0 + 256, 0);                               \
+    KG_WSTAGE(2, asx, tsx, kn, wsx, kn, wsc, k0 + 384, 0);                                                \
+    const KgWSrc wsy = lastg ? wnull : wsc;                                                               \
+    KG_WSTAGE(3, asx, tsx, kn + 128, wsy, kn + 128, wsx, kn, 0);                                          \
+    _Pragma("unroll") for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];                                   \
+    _Pragma("unroll") for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i];                                   \
+  } while (0)
+    if constexpr (MODE != 1) {
+      // (modes 0 and 2 peeled: their register allocation spills more, or at the tile start; the sums are
+      // cleared instead)
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int ks = 0; ks < KS; ks += 4) KG_WGROUP(0);
+    } else {
       {
-        const u32 keep = live_b >= 4 ? 0xffffffffu : live_b <= 0 ? 0u : (0xffffffffu >> (32 - 8 * live_b));
-        const u32 unit = 0x7f7f7f7fu & ~keep;
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) wa[0][j] = (wa[0][j] & keep) | unit;
-#pragma unroll
-        for (int i = 0; i < TI; ++i) wb[0][i] = (wb[0][i] & keep) | unit;
+        const int ks = 0;
+        KG_WGROUP(1);
       }
-      const bool lastg = ks + 4 >= KS;
-      const KgWTile wt = lastg ? nxt : cur;
-      const int kn = lastg ? 0 : (ks + 4) * 128, wkg = lastg ? 0 : (ks >> 2) + 1;
-      const KgWSrc wsx = lastg ? wsn : wsc;
-      const unsigned asx = lastg ? asn : asc;
-      const int tsx = lastg ? nxt.tail : cur.tail;
-      const int k0 = ks * 128;
-      KG_WSTAGE(0, asc, cur.tail, k0 + 256, wsc, k0 + 256, wsc, k0 + 128);
-      KG_WSTAGE(1, asc, cur.tail, k0 + 384, wsc, k0 + 384, wsc, k0 + 256);
-      KG_WSTAGE(2, asx, tsx, kn, wsx, kn, wsc, k0 + 384);
-      const KgWSrc wsy = lastg ? wnull : wsc;
-      KG_WSTAGE(3, asx, tsx, kn + 128, wsy, kn + 128, wsx, kn);
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) wa[0][j] = wa[1][j];
-#pragma unroll
-      for (int i = 0; i < TI; ++i) wb[0][i] = wb[1][i];
+      for (int ks = 4; ks < KS; ks += 4) KG_WGROUP(0);
     }
+#undef KG_WGROUP
     // the epilogue stages through buffer 3 (the last stage's): the next DMA into it is the next tile's
     // stage 3, issued after that tile's first barrier
     if constexpr (FUSED) {

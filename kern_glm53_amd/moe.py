@@ -7,7 +7,8 @@ normed row to the block's output h, with the gate_up GEMM and `silu_moe` fused i
     gather  the routed rows of xq / xsf into mq / msf                   (kg_moe_gather)
     fc1     m-grouped gate_up with the SiLU-mul-quant epilogue -> mq2   (kg_fp8_gemm_psum_silu_quant_wf, or
             (the weights in fragment order, derived at load time)     kg_fp8_gemm_psum_silu_quant without them)
-    fc2     m-grouped down -> f2                                        (kg_fp8_gemm_psum)
+    fc2     m-grouped down -> f2                                        (kg_fp8_gemm_psum_wf, or
+            (the weights in fragment order, derived at load time)     kg_fp8_gemm_psum without them)
     shared  gate_up with the SiLU-mul-quant epilogue (one group: rows   (kg_fp8_gemm_psum_silu_quant,
             [0, T)), down on xq -> sh                                    kg_fp8_gemm)
             (a chunk of x_rows not a multiple of 128: the dense gate_up  (kg_fp8_gemm, kg_silu_mul_quant)
@@ -19,9 +20,9 @@ scale words for `x_rows` rows (the chunk).  Every buffer is allocated once by `M
 nothing, and with T = MoEBuffers.T (the default) every launch of the block is one of this library's kernels.  The routed-row buffers start zeroed: the GEMMs read (and never store) their padding rows.  Weights
 are the reference's operand layouts (glm_requant's output): w13 [256 * 4096][6144] with scale words
 [256 * 12][4096], w2 [256 * 6144][2048] with [256 * 4][6144], the shared expert's w_sgu [4096][6144] /
-[12][4096] and w_sdn [6144][2048] / [4][6144].  `w13f`, when given, holds w13 in fragment order
-(kern_glm53_amd.ops.fp8_weight_frag, once at load time): fc1 then loads its weight operand straight into the
-MFMA's registers (the same outputs, bit for bit).
+[12][4096] and w_sdn [6144][2048] / [4][6144].  `w13f` and `w2f`, when given, hold w13 and w2 in fragment order
+(kern_glm53_amd.ops.fp8_weight_frag, once at load time): fc1 and fc2 then load their weight operand straight into
+the MFMA's registers (the same outputs, bit for bit).
 """
 from __future__ import annotations
 
@@ -52,6 +53,7 @@ class MoEWeights:
     w_sdn: torch.Tensor
     sf_sdn: torch.Tensor
     w13f: torch.Tensor | None = None     # w13 in fragment order (optional)
+    w2f: torch.Tensor | None = None      # w2 in fragment order (optional)
 
 
 class MoEBuffers:
@@ -103,8 +105,9 @@ def moe_block(xn, xq, xsf, w: MoEWeights, b: MoEBuffers, h, T: int | None = None
     fc1(b.mq, w.w13 if w.w13f is None else w.w13f, b.msf, w.sf13, b.psum, b.mq2, b.msf2, n=2 * INTER, k=H, rows=b.mcap,
         lda=H, sfa_rows=b.mcap, sf_rows=b.mcap)
     mark("fc1_silu_quant")
-    ops.fp8_gemm_psum(b.mq2, w.w2, b.msf2, w.sf2, b.f2, b.psum, n=H, k=INTER, rows=b.mcap, lda=INTER, ldc=H,
-                      sfa_rows=b.mcap)
+    fc2 = ops.fp8_gemm_psum if w.w2f is None else ops.fp8_gemm_psum_wf
+    fc2(b.mq2, w.w2 if w.w2f is None else w.w2f, b.msf2, w.sf2, b.f2, b.psum, n=H, k=INTER, rows=b.mcap, lda=INTER,
+        ldc=H, sfa_rows=b.mcap)
     mark("fc2")
     # the shared expert's gate_up (the reference's dense fp8 GEMM into bf16, then silu_mul_quant) as the
     # grouped GEMM with the fused epilogue over one group of T rows: the same codes and scale words (the fused

@@ -139,11 +139,14 @@ def test_moe_block_against_oracle_chain(T, x_rows):
     print(f"PARITY moe block with the MFMA model: {len(sample)} tokens, {equal} of {len(sample) * H} bf16 equal",
           flush=True)
 
-    # the same block with fc1 on the weights in fragment order: the same output, bit for bit
+    # the same block with fc1, then fc1 and fc2, on the weights in fragment order: the same output, bit for bit
     w13f = torch.empty_like(w13)
     ops.fp8_weight_frag(w13, w13f, w13.shape[0], H)
-    Wf = moe.MoEWeights(w_r, bias, rs, w13, sf13, w2, sf2, w_sgu, sf_sgu, w_sdn, sf_sdn, w13f=w13f)
-    out_f = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
-    moe.moe_block(xn, xq, xsf, Wf, B, out_f)
-    torch.cuda.synchronize()
-    assert torch.equal(out.view(torch.int16), out_f.view(torch.int16))
+    w2f = torch.empty_like(w2)
+    ops.fp8_weight_frag(w2, w2f, w2.shape[0], INTER)
+    for kw in (dict(w13f=w13f), dict(w13f=w13f, w2f=w2f)):
+        Wf = moe.MoEWeights(w_r, bias, rs, w13, sf13, w2, sf2, w_sgu, sf_sgu, w_sdn, sf_sdn, **kw)
+        out_f = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
+        moe.moe_block(xn, xq, xsf, Wf, B, out_f)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), out_f.view(torch.int16)), sorted(kw)
