@@ -8,11 +8,11 @@
 // Design: a workgroup of 8 wave64s owns 8 query rows (one per wave, its 32 heads as the rows of the MFMA
 // tiles, kept in registers for the whole key loop) and walks the union of their key ranges 64 keys at a
 // time.  A key block (64 keys x 128 bytes, and the 64 key scales) is copied HBM -> LDS by
-// buffer_load ... lds into one of two LDS stages (XOR-swizzled rows as in the GEMMs) and consumed as
+// buffer_load ... lds into one of three LDS stages (XOR-swizzled rows as in the GEMMs) and consumed as
 // 2 key tiles x 2 K halves of v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales).  Each lane of a 32x32
 // score tile holds one key and 16 of the 32 heads: relu and the head weight (fma) give a partial head
 // sum, v_permlane32_swap pairs the two tiles' halves, one add finishes both tiles' sums, then the key
-// scale and one store of 64 consecutive logits.  20 KB of LDS and 117 VGPRs: 2 workgroups per CU.  Eight
+// scale and one store of 64 consecutive logits.  30 KB of LDS and 127 VGPRs: 2 workgroups per CU.  Eight
 // rows per workgroup halve the key traffic into the CUs against four (3.7 against 3.8-4.1 ms at 16384 rows
 // of a 65536-key causal chunk); sixteen, one workgroup per CU, ran 4.2 ms.
 // The file is built with -fno-honor-nans, so fmaxf(x, 0) is one v_max_f32: the scores are finite
@@ -49,6 +49,7 @@ __global__ __launch_bounds__(512, 2) void kg_mqa_logits_kernel(const u8* __restr
   constexpr int BK = 64, TB = BK / 32, KEYB = BK * 128, STAGE = KEYB + 2048;
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
   __shared__ __attribute__((aligned(1024))) u8 st1[STAGE];
+  __shared__ __attribute__((aligned(1024))) u8 st2[STAGE];
   constexpr int NW = 8, NQ = BK / 8 / NW;          // waves (query rows) per workgroup; key DMAs per wave
   __shared__ unsigned srange[2][NW];
 
@@ -147,31 +148,35 @@ __global__ __launch_bounds__(512, 2) void kg_mqa_logits_kernel(const u8* __restr
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rlg, any && rel < lim ? rel * 4u : 0x80000000u, 0, 0);
   };
 
-  // Software pipeline over key blocks (two stages, two accumulator sets): the MFMAs of block i + 1 issue
-  // between the epilogue steps of block i, so the matrix pipe and the VALU overlap.  Per block:
+  // Software pipeline over key blocks (three stages, two accumulator sets): the MFMAs of block i + 1 issue
+  // between the epilogue steps of block i (the matrix pipe and the VALU take turns on a SIMD, so this fills
+  // issue gaps rather than overlapping the two).  Per block:
   //   read block i's key scales (its stage);
-  //   barrier: vmcnt(0), i.e. the DMA of block i + 1 and the store of block i - 2's logits (both issued right
-  //            after the previous barrier, a block ago) are complete, and every wave is done reading block i's
-  //            stage.  vmcnt counts loads and stores together and the two may complete out of order with
-  //            respect to each other, so with a store in flight only vmcnt(0) shows that a load has landed;
-  //            issuing the store ahead of the DMA gives both a whole block to complete before that wait;
-  //   the store of block i - 1's logits, the DMA of block i + 2 into block i's stage, then the MFMAs of
+  //   barrier: vmcnt(2), i.e. the DMA of block i + 1, issued two blocks ago, has landed: the loads issued
+  //            after it are the 2 DMA instructions of block i + 2, and loads complete in issue order, so with
+  //            that DMA outstanding more than 2 operations are; a store in flight (which may complete in any
+  //            order with the loads) only lengthens the wait.  lgkmcnt(0) and the barrier: every wave is
+  //            done reading block i's stage;
+  //   the store of block i - 1's logits, the DMA of block i + 3 into block i's stage, then the MFMAs of
   //   block i + 1 interleaved with block i's epilogue, whose logits are stored after the next barrier.
-  // The last block's MFMAs of the following stage run on whatever it holds and are discarded.
+  // The DMA goes out two blocks ahead (the keys come from the MALL; one block ahead, with two stages, ran
+  // 3.73 ms against 3.64 at 16384 rows of a 65536-key causal chunk, the logits identical).  The last block's
+  // MFMAs of the following stage run on whatever it holds and are discarded.
   v16f acc0[TB], acc1[TB];
   issue(st0, kmin);
   issue(st1, kmin + BK);                         // (past kmax or num_kv: read, never stored)
-  asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
-  static_assert(NQ == 1 && TB == 2, "the prologue's wait counts 2 DMA instructions per block");
+  issue(st2, kmin + 2 * BK);
+  asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  static_assert(NQ == 1 && TB == 2, "the waits count 2 DMA instructions per block");
 #pragma unroll
   for (int t = 0; t < TB; ++t) mfma(st0, acc0[t], t);
 
 #define KG_MQA_BLOCK(CUR, NXT, AC, AN)                                                                      \
   do {                                                                                                    \
     const float sc_ = *reinterpret_cast<const float*>((CUR) + KEYB + lane * 4);                           \
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");                              \
+    asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");                              \
     store(vp, kbp, anyp);                                                                                 \
-    issue(CUR, kb + 2 * BK);                                                                              \
+    issue(CUR, kb + 3 * BK);                                                                              \
     __builtin_amdgcn_sched_barrier(0);             /* the store and the DMA go out first */               \
     mfma(NXT, AN[0], 0);                                                                                  \
     const float h0_ = hsum(AC[0]);                                                                        \
@@ -182,15 +187,19 @@ __global__ __launch_bounds__(512, 2) void kg_mqa_logits_kernel(const u8* __restr
     anyp = true;                                                                                          \
     kb += BK;                                                                                             \
   } while (0)
-  // Blocks go in pairs with one exit test per pair, so that each block is one basic block and its MFMAs
-  // stay between its epilogue steps; a pair's second block may lie past kmax: its keys are past every
-  // row's ke, so its store drops.
+  // Blocks go in sixes (three stages, two accumulator sets) with one exit test per six, so that each block is
+  // one basic block and its MFMAs stay between its epilogue steps; up to five blocks may lie past kmax: their
+  // keys are past every row's ke, so their stores drop.
   unsigned kb = kmin, kbp = kmin;
   float vp = 0.0f;
   bool anyp = false;                             // no logits computed before the first block
   KG_MQA_BLOCK(st0, st1, acc0, acc1);
   while (kb < kmax) {
-    KG_MQA_BLOCK(st1, st0, acc1, acc0);
+    KG_MQA_BLOCK(st1, st2, acc1, acc0);
+    KG_MQA_BLOCK(st2, st0, acc0, acc1);
+    KG_MQA_BLOCK(st0, st1, acc1, acc0);
+    KG_MQA_BLOCK(st1, st2, acc0, acc1);
+    KG_MQA_BLOCK(st2, st0, acc1, acc0);
     KG_MQA_BLOCK(st0, st1, acc0, acc1);
   }
 #undef KG_MQA_BLOCK

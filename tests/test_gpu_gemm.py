@@ -542,10 +542,11 @@ def test_mqa_logits_ragged():
     check_mqa(out, q8, k8, ksf, w, ks, ke, stride)
 
 
-@pytest.mark.parametrize("num_kv", [50, 64, 65, 129])
+@pytest.mark.parametrize("num_kv", [50, 64, 65, 129, 200, 320, 385])
 def test_mqa_logits_short(num_kv):
-    """Key ranges of one or two 64-key blocks (the loop runs blocks in pairs: the extra block stores nothing)."""
-    num_q, stride = 6, 160
+    """Key ranges of one to seven 64-key blocks (the loop runs blocks in sixes after the first: the blocks past
+    the last key store nothing)."""
+    num_q, stride = 6, max(160, num_kv)
     q8, k8, ksf, w = mqa_case(num_q, num_kv, 55 + num_kv)
     rng = np.random.default_rng(num_kv)
     ks = rng.integers(0, num_kv, num_q)
