@@ -10,7 +10,8 @@
 //     (100 VGPRs, 32 KB of LDS each) overlap each other's copies, which beat two double-buffered
 //     workgroups per CU by 12-24%;
 //   * v_mfma_f32_32x32x16_bf16 with B (the head's weight rows, n) as the first operand and A (rows r) as
-//     the second, so each lane holds 4 consecutive d of one row: 8-byte stores;
+//     the second, so each lane holds 4 consecutive d of one row; the bf16 epilogue stages them through LDS
+//     and stores whole 128-byte row pieces, 16 bytes a lane;
 //   * buffer resources bound every operand (row offsets in the range-checked VGPR offset), so M / N tails
 //     read as zero and need no clamping.
 #include "kg_device.h"
@@ -328,7 +329,7 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
 
   if constexpr (F32OUT) {
     // lane (lane & 31, lane >> 5) holds columns 8 c + 4 (lane >> 5) .. + 3 of row 32 j + (lane & 31) of its
-    // wave's block, c = 4 i + rr: one 16-byte (f32) or 8-byte (bf16) store each
+    // wave's block, c = 4 i + rr: one 16-byte store each
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int r = m0 + wm * 32 * TJ + j * 32 + (lane & 31);
@@ -338,17 +339,10 @@ __global__ __launch_bounds__((BM / (32 * TJ)) * (BN / (32 * TI)) * 64, 1) void k
         for (int rr = 0; rr < 4; ++rr) {
           const int dn = n0 + wn * 32 * TI + (i * 4 + rr) * 8 + (lane >> 5) * 4;
           if (r < p.m && dn < p.n) {
-            if constexpr (F32OUT) {
-              float4 o;
-              o.x = acc[i][j][rr * 4 + 0], o.y = acc[i][j][rr * 4 + 1], o.z = acc[i][j][rr * 4 + 2];
-              o.w = acc[i][j][rr * 4 + 3];
-              *reinterpret_cast<float4*>(p.d + (size_t)r * p.d_rs + 4 * dn) = o;
-            } else {
-              uint2 o;
-              o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
-              o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
-              *reinterpret_cast<uint2*>(p.d + (size_t)r * p.d_rs + 2 * dn) = o;
-            }
+            float4 o;
+            o.x = acc[i][j][rr * 4 + 0], o.y = acc[i][j][rr * 4 + 1], o.z = acc[i][j][rr * 4 + 2];
+            o.w = acc[i][j][rr * 4 + 3];
+            *reinterpret_cast<float4*>(p.d + (size_t)r * p.d_rs + 4 * dn) = o;
           }
         }
     }
