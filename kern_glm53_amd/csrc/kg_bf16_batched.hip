@@ -4,11 +4,17 @@
 //
 // HBM-bound (102-169 flop/B against a bf16 ridge of ~315): the design goal is streaming A and D once at
 // full width while the MFMA work hides under it.
-//   * a workgroup = 4 wave64s owns a 128-row x 128-column tile of one head; K advances 64 (128 bytes of a
-//     row) per stage through one 32 KB LDS stage, copied HBM -> LDS by buffer_load ... lds with the same
-//     XOR-swizzled 128-byte rows as the fp8 GEMM.  K is short here (192 or 512): four workgroups per CU
-//     (100 VGPRs, 32 KB of LDS each) overlap each other's copies, which beat two double-buffered
-//     workgroups per CU by 12-24%;
+//   * a workgroup = 4 wave64s owns a 128-row x BN-column tile of one head; K advances 64 (128 bytes of a
+//     row) per stage through one LDS stage, copied HBM -> LDS by buffer_load ... lds with the same
+//     XOR-swizzled 128-byte rows as the fp8 GEMM.  K is short here (192 or 512), so the workgroups on a CU
+//     overlap each other's copies instead of double-buffering their own (four workgroups of 128 x 128 beat two
+//     double-buffered ones by 12-24%);
+//   * BN = 256 from n = 256 on (W_UK's 512 columns, W_UV's 256): a tile's operand rows through the L1s are
+//     (128 + 256) per 128 x 256 outputs, a third fewer per output than 128 x 128 tiles move, and three
+//     workgroups fit a CU (168 VGPRs, 48 KB of LDS).  At the bench shapes (one box, A/B) W_UK ran 0.407 ->
+//     0.353 ms, its K 128 form 0.321 -> 0.284 and W_UV 0.401 -> 0.359 (outputs identical: each output's MFMA
+//     chain is unchanged); 256 x 256 tiles of 8 waves (one workgroup per CU) ran 9-13% slower than 128 x 128.
+//     Below n = 256, BN = 128 (100 VGPRs, 32 KB: four workgroups per CU);
 //   * v_mfma_f32_32x32x16_bf16 with B (the head's weight rows, n) as the first operand and A (rows r) as
 //     the second, so each lane holds 4 consecutive d of one row; the bf16 epilogue stages them through LDS
 //     and stores whole 128-byte row pieces, 16 bytes a lane;
@@ -47,9 +53,12 @@ KG_DEV v8bf kg_lds_bf16x8(const u8* p) {
 }
 
 // F32OUT: the accumulators are stored as f32 (the cuBLAS f32-output GEMM the router uses) instead of bf16.
-template <bool F32OUT>
-__global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Args p) {
-  constexpr int BM = 128, BN = 128, TI = 2, TJ = 2, SA = BM * 128, STAGE = (BM + BN) * 128;
+// BN: the tile's columns, 128 or 256 (each wave 64 rows x BN / 2 columns).
+template <bool F32OUT, int BN>
+__global__ __launch_bounds__(256, BN == 256 ? 3 : 4) void kg_bf16_batched_kernel(const KgBf16Args p) {
+  static_assert(BN == 128 || BN == 256, "tile columns");
+  constexpr int BM = 128, TI = BN / 64, TJ = 2, SA = BM * 128, STAGE = (BM + BN) * 128;
+  constexpr int QB = BN / 32;                      // B DMA instructions per wave and stage
   __shared__ __attribute__((aligned(1024))) u8 st0[STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -104,12 +113,17 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
   // tile's live rows then read zeros), and only the K offset, which stays inside a row, in the scalar one.
   auto issue = [&](u8* stage, int kt) {
     const int ko = kt * 128;
+    // A's rows (the HBM stream) first, then B's (L2-resident): interleaving the two ran W_UK 9% slower
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const unsigned r = (unsigned)((wave * 4 + q) * 8);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (KG_LDS void*)(stage + (wave * 4 + q) * 1024), 16,
                                                va[q & 1] + r * (unsigned)p.a_rs, ko, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * 4 + q) * 1024), 16,
+    }
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const unsigned r = (unsigned)((wave * QB + q) * 8);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (KG_LDS void*)(stage + SA + (wave * QB + q) * 1024), 16,
                                                vb[q & 1] + r * (unsigned)p.b_rs, ko, 0, 0);
     }
   };
@@ -160,33 +174,36 @@ __global__ __launch_bounds__(256, 4) void kg_bf16_batched_kernel(const KgBf16Arg
     return;
   }
 
-  // Epilogue through LDS: each wave stages its 64 x 64 outputs (rows m, 128-byte rows, 16-byte chunk c in
-  // slot c ^ (m & 7)) in the stage (free: the K loop ends with a barrier), then stores 16 bytes per lane,
-  // 8 lanes per row: the 128-byte row pieces of D are whole cache lines (D's byte strides are multiples of
-  // 128 at the reference's shapes).
+  // Epilogue through LDS: each wave stages its outputs 64 x 64 at a time (rows m, 128-byte rows, 16-byte
+  // chunk c in slot c ^ (m & 7)) in its 8 KB of the stage (free: the K loop ends with a barrier), then stores
+  // 16 bytes per lane, 8 lanes per row: the 128-byte row pieces of D are whole cache lines (D's byte strides
+  // are multiples of 128 at the reference's shapes).  No wait between a round's writes and its reads, nor
+  // before the next round's writes: one wave's LDS operations execute in issue order.
   u8* const stg = st0 + wave * 8192;
 #pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int m = j * 32 + (lane & 31);
+  for (int ch = 0; ch < TI / 2; ++ch) {
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int j = 0; j < TJ; ++j) {
+      const int m = j * 32 + (lane & 31);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int c = i * 4 + rr;
-        uint2 o;
-        o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
-        o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
-        *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
-      }
-  }
-  // no wait before the reads: one wave's LDS operations execute in issue order, so they see its own writes
+      for (int il = 0; il < 2; ++il)
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
-    const uint4 v = *reinterpret_cast<const uint4*>(stg + m * 128 + ((c ^ (m & 7)) << 4));
-    const int r = m0 + wm * (BM / 2) + m, dn = n0 + wn * (BN / 2) + c * 8;
-    if (r < p.m && dn < p.n)
-      *reinterpret_cast<uint4*>(p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs + 2 * dn) = v;
+        for (int rr = 0; rr < 4; ++rr) {
+          const int c = il * 4 + rr, i = 2 * ch + il;
+          uint2 o;
+          o.x = kg_pack_bf16x2(acc[i][j][rr * 4 + 0], acc[i][j][rr * 4 + 1]);
+          o.y = kg_pack_bf16x2(acc[i][j][rr * 4 + 2], acc[i][j][rr * 4 + 3]);
+          *reinterpret_cast<uint2*>(stg + m * 128 + ((c ^ (m & 7)) << 4) + ((lane >> 5) << 3)) = o;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int idx = t * 64 + lane, m = idx >> 3, c = idx & 7;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + m * 128 + ((c ^ (m & 7)) << 4));
+      const int r = m0 + wm * (BM / 2) + m, dn = n0 + wn * (BN / 2) + ch * 64 + c * 8;
+      if (r < p.m && dn < p.n)
+        *reinterpret_cast<uint4*>(p.d + (size_t)r * p.d_rs + (size_t)h * p.d_hs + 2 * dn) = v;
+    }
   }
 }
 
@@ -574,20 +591,28 @@ static int kg_bf16_launch(bool f32out, const void* a, const void* b, void* d, in
   KG_CHECK(a_rs % 16 == 0 && a_hs % 16 == 0 && b_rs % 16 == 0 && b_hs % 16 == 0 && d_rs % 16 == 0 &&
            d_hs % 16 == 0);
   KG_CHECK(kg_aligned(a, 16) && kg_aligned(b, 16) && kg_aligned(d, 16));
-  KG_CHECK(a_rs >= 2ll * k && b_rs >= 2ll * k && 128ll * a_rs < (1ll << 31) && 128ll * b_rs < (1ll << 31));
+  // 128 x 256 tiles from n = 256 on (W_UK, W_UV): a third less operand fill per output than 128 x 128
+  const int bn = n >= 256 ? 256 : 128;
+  // every row offset of a tile's DMA fits the resource's 31-bit range
+  KG_CHECK(a_rs >= 2ll * k && b_rs >= 2ll * k && 128ll * a_rs < (1ll << 31) && (long long)bn * b_rs < (1ll << 31));
   if (m == 0) return 0;
   KgBf16Args p{};
   p.a = (const u8*)a, p.b = (const u8*)b, p.d = (u8*)d;
   p.a_rs = a_rs, p.a_hs = a_hs, p.b_rs = b_rs, p.b_hs = b_hs, p.d_rs = d_rs, p.d_hs = d_hs;
   p.m = m, p.n = n, p.k = k, p.heads = heads;
-  p.m_tiles = (m + 127) / 128, p.n_tiles = (n + 127) / 128;
+  p.m_tiles = (m + 127) / 128, p.n_tiles = (n + bn - 1) / bn;
   p.hg = heads % 8 == 0 ? heads / 8 : heads;
   const long long total = (long long)heads * p.m_tiles * p.n_tiles;
   KG_CHECK(total < (1ll << 31));
-  if (f32out)
-    hipLaunchKernelGGL(kg_bf16_batched_kernel<true>, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL(kg_bf16_batched_kernel<false>, dim3((unsigned)total), dim3(256), 0, (hipStream_t)stream, p);
+  const dim3 grid((unsigned)total), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  if (f32out) {
+    if (bn == 256) hipLaunchKernelGGL((kg_bf16_batched_kernel<true, 256>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((kg_bf16_batched_kernel<true, 128>), grid, block, 0, st, p);
+  } else {
+    if (bn == 256) hipLaunchKernelGGL((kg_bf16_batched_kernel<false, 256>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((kg_bf16_batched_kernel<false, 128>), grid, block, 0, st, p);
+  }
   return (int)hipGetLastError();
 }
 

@@ -64,3 +64,18 @@ def test_fragment_order_gemm_modes_spill_only_in_the_epilogue(tmp_path):
         m = meta[name]
         assert m["agpr_count"] == 256, (mode, m)
         assert m["vgpr_spill_count"] <= 12, (mode, m)
+
+
+def test_batched_gemm_fits_its_occupancy(tmp_path):
+    """The head-batched bf16 kernel (kern_glm53_amd/csrc/kg_bf16_batched.hip) relies on several workgroups per
+    CU overlapping each other's copies: 128 x 128 tiles four (at most 128 registers a lane, 32 KB of LDS),
+    128 x 256 tiles three (at most 168 registers, 48 KB), with no spills."""
+    meta = _kernel_meta(_asm(tmp_path, "kg_bf16_batched.hip"))
+    for f32 in (0, 1):
+        for bn, regs, lds in ((128, 128, 32768), (256, 168, 49152)):
+            name = f"_Z22kg_bf16_batched_kernelILb{f32}ELi{bn}EEv10KgBf16Args"
+            assert name in meta, sorted(meta)
+            m = meta[name]
+            assert m["vgpr_count"] + m["agpr_count"] <= regs, (name, m)
+            assert m["vgpr_spill_count"] == 0 and m["sgpr_spill_count"] == 0, (name, m)
+            assert m["group_segment_fixed_size"] == lds, (name, m)
