@@ -83,7 +83,8 @@ int kg_fp8_gemm_psum_silu_quant_wf(const void* a, const void* wf, const void* sf
  * accumulation, r < m, h < heads.  Every operand is a byte-strided view: element (r, h, x) of A at
  * a + r*a_rs + h*a_hs + 2x, of B (h, d, x) at b + d*b_rs + h*b_hs + 2x, of D (r, h, d) at d + r*d_rs +
  * h*d_hs + 2d.  Requires k % 64 == 0, n % 8 == 0, all strides multiples of 16 bytes, 16-byte aligned
- * base pointers (the reference's W_UK has k = 192, W_UV k = 512). */
+ * base pointers, a_rs, b_rs >= 2k, and 128*a_rs, 128*b_rs (256*b_rs when n >= 256) below 2^31 (the reference's
+ * W_UK has k = 192, W_UV k = 512). */
 int kg_bf16_batched(const void* a, const void* b, void* d, int m, int n, int k, int rows, int heads,
                     long long a_rs, long long a_hs, long long b_rs, long long b_hs, long long d_rs, long long d_hs,
                     void* stream);
