@@ -412,7 +412,7 @@ def time_launch(fn, stream, iters=7):
 
 
 def sclk_files():
-    """The sysfs DPM tables of the box's GPUs (`pp_dpm_sclk`: one line per level, the current one marked '*')."""
+    """The sysfs DPM tables of this machine's GPUs (`pp_dpm_sclk`: one line per level, the current one marked '*')."""
     import glob
     return sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
 

@@ -11,7 +11,7 @@
 //     double-buffered ones by 12-24%);
 //   * BN = 256 from n = 256 on (W_UK's 512 columns, W_UV's 256): a tile's operand rows through the L1s are
 //     (128 + 256) per 128 x 256 outputs, a third fewer per output than 128 x 128 tiles move, and three
-//     workgroups fit a CU (168 VGPRs, 48 KB of LDS).  At the bench shapes (one box, A/B) W_UK ran 0.407 ->
+//     workgroups fit a CU (168 VGPRs, 48 KB of LDS).  At the bench shapes (one MI355X, A/B) W_UK ran 0.407 ->
 //     0.353 ms, its K 128 form 0.321 -> 0.284 and W_UV 0.401 -> 0.359 (outputs identical: each output's MFMA
 //     chain is unchanged); 256 x 256 tiles of 8 waves (one workgroup per CU) ran 9-13% slower than 128 x 128.
 //     Below n = 256, BN = 128 (100 VGPRs, 32 KB: four workgroups per CU);

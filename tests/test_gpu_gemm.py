@@ -360,7 +360,7 @@ def test_bf16_batched_bench_shapes_sampled():
 
 
 def test_bf16_batched_k128_bench_shape_sampled():
-    """BASELINE's W_UK statement at full size: 64 heads x [16384 x 128] . [128 x 512], contiguous operands (the
+    """W_UK in its contiguous K 128 form at full size: 64 heads x [16384 x 128] . [128 x 512] (the
     bench's aux.w_uk_k128_bf16_batched launch); tile-edge and random rows of every head against the oracle,
     every column, and the rows past m untouched."""
     M, rows = 16384, 16384 + 64
